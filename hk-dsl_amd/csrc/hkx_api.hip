@@ -1,0 +1,458 @@
+// The C ABI of libhkx.so (include/hkx.h): argument checks, the plan of launches for a
+// call, and the launches on the caller's stream. Stateless and reentrant; the only
+// state is each thread's last error message.
+//
+// A call is the launches hk.templates.gemm's prepare() makes for a plan
+// (python/hk/templates/gemm.py:577-665): one GEMM kernel that carries the epilogue, or
+// a GEMM kernel that stores fp32 shares and a reduction that sums them in order and
+// runs the epilogue once (gemm.py:500-502; python/hk/ops/gemm_cdna_dp.py:295-324).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "hkx.h"
+#include "hkx_launch.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int elem_bytes(int dt) {
+  switch (dt) {
+    case HKX_BF16:
+    case HKX_FP16: return 2;
+    case HKX_FP32: return 4;
+    case HKX_FP8E4M3:
+    case HKX_INT8: return 1;
+    default: return 0;
+  }
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// A call resolved: which kernel, its shape parameters, how C leaves it.
+struct Plan {
+  int kernel;     // HKX_KERNEL_TILE / _DECODE
+  int tile_m, tile_n, wm;
+  int waves, fn, mf;  // decode
+  int splits;     // effective (no empty split)
+  int kunits;     // TILE: 128-byte K stages; DECODE: 128-element K groups
+  int kper;       // units per split
+  bool pair;
+  bool via_ws;    // fp32 shares / sum to ws, then the reduction
+  size_t ws_bytes;
+};
+
+bool tile_shape_ok(int bm, int bn) {
+  return (bm == 256 && bn == 256) || (bm == 128 && bn == 256) || (bm == 64 && bn == 256) ||
+         (bm == 128 && bn == 128) || (bm == 256 && bn == 128);
+}
+
+int wave_rows(int bm, int bn) {  // waves along M for a tile shape
+  if (bm == 64) return 1;
+  if (bm == 256 && bn == 128) return 4;
+  return 2;
+}
+
+// The choice hkx_gemm makes for HKX_KERNEL_AUTO; the Python layer (hk.ops.gemm_cdna.route)
+// normally passes an explicit one.
+void auto_choose(const HkxGemmArgs* a, int* kernel, int* bm, int* bn, int* splits) {
+  const int m = a->m, n = a->n;
+  const bool pair = a->ep.form == HKX_EP_SILU_MUL;
+  if (m <= 32 && a->ab_dtype == HKX_BF16 && (a->k % 128) == 0) {
+    *kernel = HKX_KERNEL_DECODE;
+    *bm = 0; *bn = 0;
+    const int per_wg = pair ? 16 : 16;
+    const int wgs = (n + per_wg - 1) / per_wg;
+    *splits = wgs >= 512 ? 1 : (wgs >= 128 ? 4 : 8);
+    return;
+  }
+  *kernel = HKX_KERNEL_TILE;
+  *bm = m <= 64 ? 64 : (m <= 128 ? 128 : 256);
+  *bn = 256;
+  const int outw = pair ? *bn / 2 : *bn;
+  const long tiles = (long)((m + *bm - 1) / *bm) * ((n + outw - 1) / outw);
+  const int kunits = a->k * elem_bytes(a->ab_dtype) / 128;
+  int s = 1;
+  while (tiles * s * 2 <= 256 && kunits / (s * 2) >= 8) s *= 2;
+  *splits = s;
+}
+
+int check_operand(const HkxOperand& o, int i) {
+  if (!o.ptr) return fail(HKX_ERR_ARG, "epilogue operand %d: null pointer", i);
+  if (o.kind != HKX_ROW && o.kind != HKX_COL && o.kind != HKX_TILE)
+    return fail(HKX_ERR_ARG, "epilogue operand %d: kind %d is not ROW, COL or TILE", i, o.kind);
+  const int eb = (o.dtype == HKX_BF16 || o.dtype == HKX_FP16) ? 2 : (o.dtype == HKX_FP32 ? 4 : 0);
+  if (!eb)
+    return fail(HKX_ERR_DTYPE, "epilogue operand %d: dtype %d; operands are bf16, fp16 or fp32", i,
+                o.dtype);
+  const size_t vec = 4 * eb;  // four elements are loaded at once
+  if (o.kind == HKX_ROW && o.ld != 0 && !aligned(o.ptr, vec))
+    return fail(HKX_ERR_SHAPE, "epilogue operand %d: a row vector must be %zu-byte aligned", i, vec);
+  if (o.kind == HKX_TILE && (!aligned(o.ptr, vec) || (o.ld * eb) % vec || o.ld < 0))
+    return fail(HKX_ERR_SHAPE,
+                "epilogue operand %d: a tile operand must be %zu-byte aligned, rows too", i, vec);
+  if (o.kind == HKX_COL && (o.ld < 0 || !aligned(o.ptr, eb)))
+    return fail(HKX_ERR_SHAPE, "epilogue operand %d: a column vector needs a row stride >= 0", i);
+  return HKX_OK;
+}
+
+int check_epilogue(const HkxEpilogue& ep) {
+  if (ep.nops < 0 || ep.nops > HKX_MAX_OPERANDS)
+    return fail(HKX_ERR_ARG, "epilogue: %d operands (at most %d)", ep.nops, HKX_MAX_OPERANDS);
+  for (int i = 0; i < ep.nops; ++i) {
+    int rc = check_operand(ep.ops[i], i);
+    if (rc) return rc;
+  }
+  switch (ep.form) {
+    case HKX_EP_NONE:
+    case HKX_EP_SILU_MUL: return HKX_OK;
+    case HKX_EP_FUSED: {
+      const int idx[4] = {ep.col_scale, ep.row_scale, ep.row_add, ep.tile_add};
+      const int kind[4] = {HKX_COL, HKX_ROW, HKX_ROW, HKX_TILE};
+      const char* what[4] = {"col_scale", "row_scale", "row_add", "tile_add"};
+      for (int s = 0; s < 4; ++s) {
+        if (idx[s] < -1 || idx[s] >= ep.nops)
+          return fail(HKX_ERR_ARG, "fused epilogue: %s names operand %d of %d", what[s], idx[s],
+                      ep.nops);
+        if (idx[s] >= 0 && ep.ops[idx[s]].kind != kind[s])
+          return fail(HKX_ERR_ARG, "fused epilogue: %s is operand %d, of the wrong kind", what[s],
+                      idx[s]);
+      }
+      if (ep.act < HKX_ACT_NONE || ep.act > HKX_ACT_RELU)
+        return fail(HKX_ERR_ARG, "fused epilogue: activation %d", ep.act);
+      return HKX_OK;
+    }
+    case HKX_EP_PROGRAM: {
+      if (ep.nins < 0 || ep.nins > HKX_MAX_INSTR)
+        return fail(HKX_ERR_ARG, "epilogue program: %d instructions (at most %d)", ep.nins,
+                    HKX_MAX_INSTR);
+      if (ep.out_reg < 0 || ep.out_reg >= HKX_MAX_REGS)
+        return fail(HKX_ERR_ARG, "epilogue program: output register %d", ep.out_reg);
+      for (int i = 0; i < ep.nins; ++i) {
+        const HkxInstr& I = ep.ins[i];
+        if (I.op >= HKX_NUM_OPS || I.dst >= HKX_MAX_REGS || I.a >= HKX_MAX_REGS ||
+            I.b >= HKX_MAX_REGS || I.c >= HKX_MAX_REGS)
+          return fail(HKX_ERR_ARG, "epilogue program: instruction %d is malformed", i);
+        if (I.op == HKX_OP_LOAD && I.a >= ep.nops)
+          return fail(HKX_ERR_ARG, "epilogue program: instruction %d loads operand %d of %d", i,
+                      I.a, ep.nops);
+      }
+      return HKX_OK;
+    }
+    default: return fail(HKX_ERR_ARG, "epilogue form %d", ep.form);
+  }
+}
+
+int make_plan(const HkxGemmArgs* a, Plan* p) {
+  if (!a) return fail(HKX_ERR_ARG, "null args");
+  if (!a->a || !a->b || !a->c) return fail(HKX_ERR_ARG, "A, B and C must be device pointers");
+  if (a->m < 1 || a->k < 1 || a->n < 1)
+    return fail(HKX_ERR_SHAPE, "M=%d, N=%d, K=%d; nothing to multiply", a->m, a->n, a->k);
+  if (a->ab_dtype != HKX_BF16 && a->ab_dtype != HKX_FP8E4M3)
+    return fail(HKX_ERR_DTYPE, "A and B are bf16 or fp8-e4m3 (dtype %d)", a->ab_dtype);
+  const int ob = elem_bytes(a->c_dtype);
+  if (!ob) return fail(HKX_ERR_DTYPE, "C dtype %d", a->c_dtype);
+  const int eb = elem_bytes(a->ab_dtype);
+  const int kstep = 128 / eb;
+  if (a->k % kstep || a->n % 4)
+    return fail(HKX_ERR_SHAPE, "K=%d must be a multiple of %d and N=%d of 4; M may be anything",
+                a->k, kstep, a->n);
+  if (a->lda < a->k || a->ldb < a->k || a->ldc < a->n)
+    return fail(HKX_ERR_SHAPE, "row strides lda=%lld ldb=%lld ldc=%lld are below K / N",
+                (long long)a->lda, (long long)a->ldb, (long long)a->ldc);
+  if (!aligned(a->a, 16) || !aligned(a->b, 16) || (a->lda * eb) % 16 || (a->ldb * eb) % 16)
+    return fail(HKX_ERR_SHAPE, "A and B need 16-byte aligned rows (base and row stride)");
+  if (!aligned(a->c, 4 * ob) || a->ldc % 4)
+    return fail(HKX_ERR_SHAPE, "C needs %d-byte alignment and a row stride a multiple of 4",
+                4 * ob);
+  const bool pair = a->ep.form == HKX_EP_SILU_MUL;
+  const long long brows = pair ? 2LL * a->n : a->n;
+  if ((long long)a->m * a->lda * eb >= (1LL << 32) || brows * a->ldb * eb >= (1LL << 32))
+    return fail(HKX_ERR_SHAPE, "A or B spans 4 GiB or more; split the call");
+  int rc = check_epilogue(a->ep);
+  if (rc) return rc;
+
+  int kernel = a->kernel, bm = a->tile_m, bn = a->tile_n, splits = a->splits;
+  if (kernel == HKX_KERNEL_AUTO) auto_choose(a, &kernel, &bm, &bn, &splits);
+  if (splits < 1) splits = 1;
+  p->kernel = kernel;
+  p->pair = pair;
+  if (kernel == HKX_KERNEL_TILE) {
+    if (!tile_shape_ok(bm, bn))
+      return fail(HKX_ERR_ARG, "tile %dx%d: 256x256, 128x256, 64x256, 128x128 or 256x128", bm, bn);
+    p->tile_m = bm;
+    p->tile_n = bn;
+    p->wm = wave_rows(bm, bn);
+    p->kunits = a->k * eb / 128;
+  } else if (kernel == HKX_KERNEL_DECODE) {
+    if (a->ab_dtype != HKX_BF16) return fail(HKX_ERR_DTYPE, "the decode kernel takes bf16");
+    if (a->m > 32) return fail(HKX_ERR_SHAPE, "the decode kernel takes M <= 32 (M=%d)", a->m);
+    if (a->k % 128) return fail(HKX_ERR_SHAPE, "the decode kernel takes K a multiple of 128");
+    p->waves = a->decode_waves ? a->decode_waves : 8;
+    const int rows = a->decode_rows ? a->decode_rows : (pair ? 32 : 16);
+    if (p->waves != 4 && p->waves != 8 && p->waves != 16)
+      return fail(HKX_ERR_ARG, "decode waves %d: 4, 8 or 16", p->waves);
+    if (rows != 16 && rows != 32) return fail(HKX_ERR_ARG, "decode rows %d: 16 or 32", rows);
+    if (pair && rows != 32) return fail(HKX_ERR_ARG, "the paired decode kernel takes 32 rows");
+    p->fn = rows / 16;
+    p->mf = a->m <= 16 ? 1 : 2;
+    p->kunits = a->k / 128;
+  } else {
+    return fail(HKX_ERR_ARG, "kernel %d", kernel);
+  }
+  if (splits > p->kunits) splits = p->kunits;
+  p->kper = (p->kunits + splits - 1) / splits;
+  p->splits = (p->kunits + p->kper - 1) / p->kper;
+
+  // Shares (or one fp32 sum) go through the workspace when the K sum is split, when
+  // the epilogue is a program, or when a paired C is not 16-bit (tile kernel).
+  const bool program = a->ep.form == HKX_EP_PROGRAM;
+  bool ws = p->splits > 1 || program;
+  if (pair && kernel == HKX_KERNEL_TILE && ob != 2) ws = true;
+  p->via_ws = ws;
+  const long long wcols = pair ? 2LL * a->n : a->n;
+  p->ws_bytes = ws ? (size_t)p->splits * a->m * wcols * sizeof(float) : 0;
+  if (ws && (!a->ws || a->ws_bytes < p->ws_bytes || !aligned(a->ws, 16)))
+    return fail(HKX_ERR_WORKSPACE, "this plan needs a 16-byte aligned fp32 workspace of %zu bytes",
+                p->ws_bytes);
+  return HKX_OK;
+}
+
+hkx::Fused make_fused(const HkxEpilogue& ep) {
+  hkx::Fused f{};
+  f.form = ep.form == HKX_EP_FUSED ? HKX_EP_FUSED : HKX_EP_NONE;
+  f.cmul = 1.0f;
+  if (ep.form != HKX_EP_FUSED) return f;
+  auto opnd = [&](int i) {
+    hkx::Opnd o{};
+    if (i >= 0) {
+      o.p = ep.ops[i].ptr;
+      o.ld = ep.ops[i].ld;
+      o.dt = ep.ops[i].dtype;
+      o.kind = ep.ops[i].kind;
+    }
+    return o;
+  };
+  f.cs = opnd(ep.col_scale);
+  f.rs = opnd(ep.row_scale);
+  f.ra = opnd(ep.row_add);
+  f.ta = opnd(ep.tile_add);
+  f.cmul = ep.cmul;
+  f.cadd = ep.cadd;
+  f.act = ep.act;
+  return f;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(HKX_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return HKX_OK;
+}
+
+hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mode, dim3 grid,
+                         hipStream_t s) {
+  const int bm = p.tile_m, bn = p.tile_n;
+  if (bm == 256 && bn == 256) return hkx::launch_tile<256, 256, 2>(t, fp8, mode, grid, s);
+  if (bm == 128 && bn == 256) return hkx::launch_tile<128, 256, 2>(t, fp8, mode, grid, s);
+  if (bm == 64 && bn == 256) return hkx::launch_tile<64, 256, 1>(t, fp8, mode, grid, s);
+  if (bm == 128 && bn == 128) return hkx::launch_tile<128, 128, 2>(t, fp8, mode, grid, s);
+  return hkx::launch_tile<256, 128, 4>(t, fp8, mode, grid, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hkx_abi_version(void) { return HKX_ABI_VERSION; }
+
+void hkx_abi_sizes(size_t out[4]) {
+  out[0] = sizeof(HkxOperand);
+  out[1] = sizeof(HkxInstr);
+  out[2] = sizeof(HkxEpilogue);
+  out[3] = sizeof(HkxGemmArgs);
+}
+
+const char* hkx_last_error(void) { return g_err.c_str(); }
+
+size_t hkx_gemm_workspace(const HkxGemmArgs* args) {
+  // Plan a copy that carries an ample (never dereferenced) workspace, so the
+  // workspace check passes and only the size comes back.
+  Plan p{};
+  if (!args) return 0;
+  HkxGemmArgs a = *args;
+  a.ws = (void*)(uintptr_t)256;  // any aligned non-null pointer: only the size is wanted
+  a.ws_bytes = (size_t)-1;
+  if (make_plan(&a, &p) != HKX_OK) return 0;
+  return p.ws_bytes;
+}
+
+int hkx_gemm_check(const HkxGemmArgs* args) {
+  Plan p{};
+  g_err.clear();
+  return make_plan(args, &p);
+}
+
+int hkx_gemm(const HkxGemmArgs* args, void* stream) {
+  Plan p{};
+  g_err.clear();
+  int rc = make_plan(args, &p);
+  if (rc) return rc;
+  const HkxGemmArgs& a = *args;
+  hipStream_t s = (hipStream_t)stream;
+  const bool fp8 = a.ab_dtype == HKX_FP8E4M3;
+  const int eb = elem_bytes(a.ab_dtype);
+  const int ob = elem_bytes(a.c_dtype);
+  const long long wcols = p.pair ? 2LL * a.n : a.n;
+  const hkx::Fused fused = make_fused(a.ep);
+  const bool program = a.ep.form == HKX_EP_PROGRAM;
+
+  if (p.kernel == HKX_KERNEL_TILE) {
+    hkx::TileArgs t{};
+    t.a = a.a;
+    t.b = a.b;
+    t.a_bytes = (uint32_t)((long long)a.m * a.lda * eb);
+    t.b_bytes = (uint32_t)((p.pair ? 2LL : 1LL) * a.n * a.ldb * eb);
+    t.lda_b = (uint32_t)(a.lda * eb);
+    t.ldb_b = (uint32_t)(a.ldb * eb);
+    t.M = a.m;
+    t.N = a.n;
+    t.kt_total = p.kunits;
+    t.kt_split = p.kper;
+    const int outw = p.pair ? p.tile_n / 2 : p.tile_n;
+    t.tiles_m = (a.m + p.tile_m - 1) / p.tile_m;
+    t.tiles_n = (a.n + outw - 1) / outw;
+    t.wgm = 4;
+    t.pair_off = a.n;
+    t.c_dt = a.c_dtype;
+    const dim3 grid(t.tiles_m * t.tiles_n, p.splits);
+    int mode;
+    if (p.via_ws) {
+      t.c = a.ws;
+      t.ldc = wcols;
+      t.split_stride = (int64_t)a.m * wcols;
+      t.c_dt = HKX_FP32;
+      t.ep = hkx::Fused{};
+      t.ep.form = HKX_EP_NONE;
+      mode = p.pair ? hkx::kPairWs : hkx::kStoreF32;
+    } else {
+      t.c = a.c;
+      t.ldc = a.ldc;
+      t.split_stride = 0;
+      t.c_aligned = aligned(a.c, 16) && (a.ldc * ob) % 16 == 0;
+      t.ep = fused;
+      if (p.pair) mode = hkx::kPair16;
+      else if (ob == 2) mode = hkx::kStore16;
+      else if (ob == 1) mode = hkx::kStore8;
+      else mode = hkx::kStoreF32;
+    }
+    rc = launched(tile_dispatch(p, t, fp8, mode, grid, s), "tile GEMM");
+    if (rc) return rc;
+  } else {
+    hkx::DecodeArgs d{};
+    d.a = a.a;
+    d.b = a.b;
+    d.a_bytes = (uint32_t)((long long)a.m * a.lda * eb);
+    d.b_bytes = (uint32_t)((p.pair ? 2LL : 1LL) * a.n * a.ldb * eb);
+    d.lda_b = (uint32_t)(a.lda * eb);
+    d.ldb_b = (uint32_t)(a.ldb * eb);
+    d.M = a.m;
+    d.N = a.n;
+    d.g_total = p.kunits;
+    d.g_split = p.kper;
+    d.pair_off = a.n;
+    d.c_dt = a.c_dtype;
+    const int outw = p.pair ? 8 * p.fn : 16 * p.fn;
+    const dim3 grid((a.n + outw - 1) / outw, p.splits);
+    int mode;
+    if (p.via_ws) {
+      d.c = a.ws;
+      d.ldc = p.pair ? a.n * 2LL : a.n;
+      d.split_stride = (int64_t)a.m * wcols;
+      d.c_dt = HKX_FP32;
+      d.ep.form = HKX_EP_NONE;
+      mode = p.pair ? hkx::kDecPairWs : hkx::kDecWs;
+    } else {
+      d.c = a.c;
+      d.ldc = a.ldc;
+      d.ep = fused;
+      mode = p.pair ? hkx::kDecPair : hkx::kDecOut;
+    }
+    rc = launched(hkx::launch_decode(d, p.waves, p.fn, p.mf, mode, grid, s), "decode GEMM");
+    if (rc) return rc;
+  }
+
+  if (p.via_ws) {
+    hkx::ReduceArgs r{};
+    r.ws = (const float*)a.ws;
+    r.split_stride = (int64_t)a.m * wcols;
+    r.ws_ld = wcols;
+    r.c = a.c;
+    r.ldc = a.ldc;
+    r.splits = p.splits;
+    r.M = a.m;
+    r.N = a.n;
+    r.c_dt = a.c_dtype;
+    r.pair = p.pair;
+    r.f = fused;
+    const dim3 grid(((a.n + 3) / 4 + 255) / 256, a.m < 65535 ? a.m : 65535);
+    rc = launched(hkx::launch_reduce(r, a.ep, program, grid, s), "reduction");
+    if (rc) return rc;
+  }
+  return HKX_OK;
+}
+
+int hkx_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
+                  int64_t sa_ld, const float* scale_b, int32_t sb_per_channel, const void* bias,
+                  void* c, int64_t ldc, int32_t m, int32_t n, int32_t k, void* ws,
+                  size_t ws_bytes, void* stream) {
+  HkxGemmArgs g;
+  memset(&g, 0, sizeof g);
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = ldc;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.ab_dtype = HKX_FP8E4M3;
+  g.c_dtype = HKX_BF16;
+  g.kernel = HKX_KERNEL_AUTO;
+  g.splits = 1;
+  g.ws = ws;
+  g.ws_bytes = ws_bytes;
+  HkxEpilogue& ep = g.ep;
+  ep.form = HKX_EP_FUSED;
+  ep.act = HKX_ACT_NONE;
+  ep.cmul = 1.0f;
+  ep.col_scale = ep.row_scale = ep.row_add = ep.tile_add = -1;
+  if (!scale_a || !scale_b) return fail(HKX_ERR_ARG, "scaled_mm: scale_a and scale_b are required");
+  ep.ops[0] = HkxOperand{scale_a, HKX_COL, HKX_FP32, sa_ld};
+  ep.ops[1] = HkxOperand{scale_b, HKX_ROW, HKX_FP32, sb_per_channel ? 1 : 0};
+  ep.col_scale = 0;
+  ep.row_scale = 1;
+  ep.nops = 2;
+  if (bias) {
+    ep.ops[2] = HkxOperand{bias, HKX_ROW, HKX_BF16, 1};
+    ep.row_add = 2;
+    ep.nops = 3;
+  }
+  return hkx_gemm(&g, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// Decode GEMM kernels: 4, 8 or 16 waves, 16 or 32 rows of W a workgroup, 1 or 2
+// 16-token fragments, every store mode.
+#include "hkx_launch.hpp"
+
+namespace hkx {
+
+// Groups in flight per wave: as many as the wave's share of the register file holds
+// beside the accumulators (16 VGPRs a fragment a group, for W's and for X's).
+constexpr int decode_unroll(int waves, int fn, int mf) {
+  const int budget = 512 / (waves / 4 > 0 ? waves / 4 : 1);
+  const int u = (budget - 48) / (16 * (fn + mf));
+  return u < 1 ? 1 : (u > 4 ? 4 : u);
+}
+
+template <int NW, int FN, int MF>
+static hipError_t launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_t s) {
+  constexpr int U = decode_unroll(NW, FN, MF);
+  const dim3 block(NW * 64);
+  switch (mode) {
+    case kDecOut: hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecOut>), grid, block, 0, s, a); break;
+    case kDecWs: hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecWs>), grid, block, 0, s, a); break;
+    case kDecPair:
+      if constexpr (FN % 2 == 0) { hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecPair>), grid, block, 0, s, a); break; }
+      return hipErrorInvalidValue;
+    case kDecPairWs:
+      if constexpr (FN % 2 == 0) { hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecPairWs>), grid, block, 0, s, a); break; }
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int NW>
+static hipError_t launch_fn(const DecodeArgs& a, int fn, int mf, int mode, dim3 grid, hipStream_t s) {
+  if (fn == 1) return mf == 1 ? launch_nw<NW, 1, 1>(a, mode, grid, s) : launch_nw<NW, 1, 2>(a, mode, grid, s);
+  return mf == 1 ? launch_nw<NW, 2, 1>(a, mode, grid, s) : launch_nw<NW, 2, 2>(a, mode, grid, s);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
+                         hipStream_t s) {
+  if (waves == 4) return launch_fn<4>(a, fn, mf, mode, grid, s);
+  if (waves == 8) return launch_fn<8>(a, fn, mf, mode, grid, s);
+  return launch_fn<16>(a, fn, mf, mode, grid, s);
+}
+
+}  // namespace hkx

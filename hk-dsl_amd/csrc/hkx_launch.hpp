@@ -1,0 +1,48 @@
+// Host-side launchers of the kernel templates, one explicit instantiation set per
+// translation unit (hkx_tile_*.hip, hkx_decode.hip, hkx_reduce.hip) so the build
+// compiles them in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "hkx_decode.hpp"
+#include "hkx_reduce.hpp"
+#include "hkx_tile.hpp"
+
+namespace hkx {
+
+template <int BM, int BN, int WM>
+hipError_t launch_tile(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
+
+hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
+                         hipStream_t s);
+
+hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool program, dim3 grid,
+                         hipStream_t s);
+
+#define HKX_TILE_LAUNCHER(BM, BN, WM)                                                        \
+  template <>                                                                                \
+  hipError_t launch_tile<BM, BN, WM>(const TileArgs& a, bool fp8, int mode, dim3 grid,       \
+                                     hipStream_t s) {                                        \
+    const dim3 block(512);                                                                   \
+    if (fp8) {                                                                               \
+      switch (mode) {                                                                        \
+        case kStore16: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, true, kStore16>), grid, block, 0, s, a); break;   \
+        case kStore8: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, true, kStore8>), grid, block, 0, s, a); break;     \
+        case kStoreF32: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, true, kStoreF32>), grid, block, 0, s, a); break; \
+        default: return hipErrorInvalidValue;                                                \
+      }                                                                                      \
+    } else {                                                                                 \
+      switch (mode) {                                                                        \
+        case kStore16: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kStore16>), grid, block, 0, s, a); break;   \
+        case kStore8: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kStore8>), grid, block, 0, s, a); break;     \
+        case kStoreF32: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kStoreF32>), grid, block, 0, s, a); break; \
+        case kPair16: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kPair16>), grid, block, 0, s, a); break;     \
+        case kPairWs: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kPairWs>), grid, block, 0, s, a); break;     \
+        default: return hipErrorInvalidValue;                                                \
+      }                                                                                      \
+    }                                                                                        \
+    return hipGetLastError();                                                                \
+  }
+
+}  // namespace hkx

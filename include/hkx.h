@@ -1,0 +1,199 @@
+/*
+ * hkx.h -- the C ABI of libhkx.so: GEMM with a fused epilogue on MI355X (gfx950).
+ *
+ * C = epilogue(A . B^T accumulated in fp32), A (M, K) and B (N, K) K-contiguous
+ * (F.linear's layout), bf16 x bf16 or fp8-e4m3 x fp8-e4m3, C (M, N) in bf16, fp16,
+ * fp32, int8 or fp8-e4m3.
+ *
+ * Plain pointers and sizes only; no torch types. Every pointer is a device pointer
+ * on the current HIP device; every launch goes on the stream passed in. The library
+ * allocates nothing and never synchronizes: a caller that needs a workspace asks
+ * hkx_gemm_workspace() for its size and passes it in (HkxGemmArgs.ws).
+ *
+ * What each entry point replaces in the reference (vivienfanghuagood/hk-dsl 0.9.24):
+ *
+ *   hkx_gemm            the launches hk.templates.gemm prepares for a plan, one
+ *                       `kern(a, b, c, *extra, *ep_tensors, **consts)` per Step
+ *                       (python/hk/templates/gemm.py:577-665, launch convention
+ *                       python/hk/ops/_epilogue.py:28-43), which end in
+ *                       hipModuleLaunchKernel on the caller's stream
+ *                       (mlir/python/HKLaunch.c:1-25, python/hk/runtime/codeobj.py:265-276).
+ *                       The kernels it runs replace gemm_cdna.gemm_kernel
+ *                       (python/hk/ops/gemm_cdna.py:57-586), gemm_cdna_dp.gemm_kernel and
+ *                       its split-K shares (python/hk/ops/gemm_cdna_dp.py:30-243),
+ *                       reduce_epilogue_kernel (gemm_cdna_dp.py:295-324, 361-383) and
+ *                       decode_gemm_kernel (python/hk/ops/decode_gemm.py:37-180).
+ *   hkx_scaled_mm       hk.ops.gemm.scaled_mm's launch (python/hk/ops/gemm.py:884-975):
+ *                       bf16 (A . B^T) * scale_a * scale_b (+ bias), fp8 operands.
+ *   hkx_gemm_workspace  gemm_cdna_dp.scratch_for / decode_gemm.scratch_for
+ *                       (gemm_cdna_dp.py:330-338, decode_gemm.py:283-298): the size of
+ *                       the fp32 share buffer a plan needs (the caller allocates it).
+ *   hkx_last_error      the message the reference raises in Python (ValueError /
+ *                       TypeError texts of templates/gemm.py:770-803).
+ */
+#ifndef HKX_H_
+#define HKX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HKX_ABI_VERSION 1
+
+/* Status codes. */
+#define HKX_OK 0
+#define HKX_ERR_SHAPE 1       /* a shape / stride / alignment the kernels do not take */
+#define HKX_ERR_DTYPE 2       /* an element type the kernels do not take */
+#define HKX_ERR_WORKSPACE 3   /* ws missing or smaller than hkx_gemm_workspace() */
+#define HKX_ERR_LAUNCH 4      /* hipLaunchKernel failed; hkx_last_error() has hipGetErrorString */
+#define HKX_ERR_ARG 5         /* a malformed argument (epilogue program, operand, null pointer) */
+
+/* Element types. */
+#define HKX_BF16 0
+#define HKX_FP16 1
+#define HKX_FP32 2
+#define HKX_FP8E4M3 3 /* OCP e4m3 (float8_e4m3fn): max 448, no inf */
+#define HKX_INT8 4
+
+/* Epilogue operand kinds: what an operand is against C (M, N) -- templates/gemm.py:116-135. */
+#define HKX_ROW 1  /* (N,) or (1, N): one value per column of C (a bias, a per-channel scale) */
+#define HKX_COL 2  /* (M, 1): one value per row (a per-token scale); ld = its row stride */
+#define HKX_TILE 3 /* (M, N): one per element (a residual); ld = its row stride */
+
+/* Epilogue forms. */
+#define HKX_EP_NONE 0     /* C = acc */
+#define HKX_EP_FUSED 1    /* C = act(acc * col_scale[m] * row_scale[n] * cmul + row_add[n] + tile_add[m,n] + cadd) */
+#define HKX_EP_PROGRAM 2  /* C = the register program below, run once per element on the fp32 sum */
+#define HKX_EP_SILU_MUL 3 /* C[:, j] = silu(acc[:, j]) * acc[:, N + j]; B is (2N, K), gate rows then up rows */
+
+/* Activations of the fused form. */
+#define HKX_ACT_NONE 0
+#define HKX_ACT_GELU_TANH 1
+#define HKX_ACT_SILU 2
+#define HKX_ACT_RELU 3
+
+/* Program opcodes: dst <- f(a, b, c); registers are fp32, R0 starts as the accumulator. */
+#define HKX_OP_MOV 0    /* dst = r[a] */
+#define HKX_OP_LOAD 1   /* dst = operand a at this element (by its kind), as fp32 */
+#define HKX_OP_CONST 2  /* dst = imm */
+#define HKX_OP_ROW 3    /* dst = the element's row of C */
+#define HKX_OP_COL 4    /* dst = the element's column of C, plus col0 */
+#define HKX_OP_ADD 5
+#define HKX_OP_SUB 6
+#define HKX_OP_MUL 7
+#define HKX_OP_DIV 8
+#define HKX_OP_MAX 9
+#define HKX_OP_MIN 10
+#define HKX_OP_EXP 11
+#define HKX_OP_EXP2 12
+#define HKX_OP_LOG 13
+#define HKX_OP_LOG2 14
+#define HKX_OP_ABS 15
+#define HKX_OP_RELU 16
+#define HKX_OP_GELU 17  /* tanh approximation */
+#define HKX_OP_SILU 18
+#define HKX_OP_SQRT 19
+#define HKX_OP_RSQRT 20
+#define HKX_OP_NEG 21
+#define HKX_OP_STEP 22  /* 1 where r[a] > 0, else 0 */
+#define HKX_OP_SELLE 23 /* dst = r[a] <= 0 ? r[b] : r[c] */
+#define HKX_OP_M 24     /* dst = M (C's rows) */
+#define HKX_OP_TANH 25
+#define HKX_OP_SIGMOID 26
+#define HKX_OP_SQUARE 27 /* dst = r[a] * r[a] */
+#define HKX_NUM_OPS 28
+
+#define HKX_MAX_OPERANDS 8
+#define HKX_MAX_INSTR 64
+#define HKX_MAX_REGS 16
+
+typedef struct HkxOperand {
+  const void* ptr; /* device pointer */
+  int32_t kind;    /* HKX_ROW / HKX_COL / HKX_TILE */
+  int32_t dtype;   /* HKX_BF16 / HKX_FP16 / HKX_FP32 */
+  int64_t ld;      /* COL, TILE: row stride in elements. ROW: 1 (a vector) or 0 (one value
+                      broadcast to every column) */
+} HkxOperand;
+
+typedef struct HkxInstr {
+  uint8_t op, dst, a, b, c, pad0, pad1, pad2;
+  float imm;
+} HkxInstr;
+
+typedef struct HkxEpilogue {
+  int32_t form; /* HKX_EP_* */
+  /* HKX_EP_FUSED: operand indices into ops[] (-1 = absent), the activation, constants. */
+  int32_t act;
+  int32_t col_scale, row_scale, row_add, tile_add;
+  float cmul, cadd;
+  /* HKX_EP_PROGRAM */
+  int32_t nins;
+  int32_t out_reg;
+  int32_t col0; /* added to HKX_OP_COL (a launch on a column slice of a larger C) */
+  int32_t nops;
+  HkxOperand ops[HKX_MAX_OPERANDS];
+  HkxInstr ins[HKX_MAX_INSTR];
+} HkxEpilogue;
+
+/* Kernel families (HkxGemmArgs.kernel). */
+#define HKX_KERNEL_AUTO 0
+#define HKX_KERNEL_TILE 1   /* LDS-tiled MFMA GEMM, tile_m x tile_n blocks, optional split-K */
+#define HKX_KERNEL_DECODE 2 /* skinny-M weight-streaming GEMM (M <= 32), optional split-K */
+
+typedef struct HkxGemmArgs {
+  const void* a; /* (M, K), row stride lda elements */
+  const void* b; /* (N, K) -- (2N, K) for HKX_EP_SILU_MUL -- row stride ldb elements */
+  void* c;       /* (M, N), row stride ldc elements */
+  int64_t lda, ldb, ldc;
+  int32_t m, n, k;
+  int32_t ab_dtype; /* HKX_BF16 or HKX_FP8E4M3 (both operands) */
+  int32_t c_dtype;  /* HKX_BF16 / HKX_FP16 / HKX_FP32 / HKX_INT8 / HKX_FP8E4M3 */
+  int32_t kernel;   /* HKX_KERNEL_* */
+  int32_t tile_m;   /* TILE: 64, 128 or 256 */
+  int32_t tile_n;   /* TILE: 128 or 256 */
+  int32_t splits;   /* >= 1; > 1 stores fp32 shares to ws and sums them in order */
+  int32_t decode_waves; /* DECODE: waves per workgroup (4, 8 or 16); 0 = default */
+  int32_t decode_rows;  /* DECODE: W rows per workgroup (16 or 32); 0 = default */
+  void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */
+  size_t ws_bytes;
+  HkxEpilogue ep;
+} HkxGemmArgs;
+
+/* Library identity. */
+int hkx_abi_version(void);
+/* sizeof(HkxOperand), sizeof(HkxInstr), sizeof(HkxEpilogue), sizeof(HkxGemmArgs) into
+ * out[0..3]: lets a binding check its struct layouts against the library's. */
+void hkx_abi_sizes(size_t out[4]);
+/* The message of the last failed call on this thread ("" if none). */
+const char* hkx_last_error(void);
+
+/* Bytes of fp32 workspace hkx_gemm needs for these args (0 if none). Resolves
+ * HKX_KERNEL_AUTO the way hkx_gemm does. Host-only, needs no GPU. */
+size_t hkx_gemm_workspace(const HkxGemmArgs* args);
+
+/* Checks args (HKX_OK or an error code, message in hkx_last_error) without launching.
+ * Host-only, needs no GPU. */
+int hkx_gemm_check(const HkxGemmArgs* args);
+
+/* Launch the plan for args on stream (a hipStream_t; NULL = the null stream).
+ * Returns HKX_OK or an error code; hkx_last_error() says why. */
+int hkx_gemm(const HkxGemmArgs* args, void* stream);
+
+/* bf16 C = (A . B^T) * scale_a * scale_b (+ bias), A (M, K) and B (N, K) fp8-e4m3,
+ * scale_a fp32 with sa_ld 0 (one value for all rows: per-tensor) or its row
+ * stride (per-token, (M, 1)); scale_b fp32, sb_per_channel 0 (one value) or 1
+ * ((N,), per-channel); bias bf16 (N,) or NULL. Row strides in elements. */
+int hkx_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                  const float* scale_a, int64_t sa_ld, const float* scale_b,
+                  int32_t sb_per_channel, const void* bias, void* c, int64_t ldc,
+                  int32_t m, int32_t n, int32_t k, void* ws, size_t ws_bytes,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HKX_H_ */

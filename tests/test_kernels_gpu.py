@@ -1,0 +1,205 @@
+"""The gfx950 kernels through the C ABI (hk._native), against the CPU oracle:
+every tile shape and store mode, bf16 and fp8, split-K, the decode kernel, the paired
+silu-and-mul form and the epilogue-program pass. Inputs are made on the CPU from a
+seeded generator, so the oracle sees exactly the operands the GPU does."""
+
+import ctypes
+
+import pytest
+import torch
+
+from hk import _native as nat
+from oracle import gemm_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _data(m, n, k, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed * 1000003 + m * 7919 + n * 31 + k)
+    a = torch.randn(m, k, generator=g).to(dtype)
+    b = (torch.randn(n, k, generator=g) * k ** -0.5).to(dtype)
+    return a, b
+
+
+def _fused(ops, *, act=nat.ACT_NONE, cs=-1, rs=-1, ra=-1, ta=-1, cmul=1.0, cadd=0.0):
+    ep = nat.HkxEpilogue()
+    ep.form = nat.EP_FUSED
+    ep.act, ep.col_scale, ep.row_scale, ep.row_add, ep.tile_add = act, cs, rs, ra, ta
+    ep.cmul, ep.cadd = cmul, cadd
+    ep.nops = len(ops)
+    for i, (t, kind) in enumerate(ops):
+        ep.ops[i] = nat.HkxOperand(t.data_ptr(), kind, nat.dtype_code(t.dtype),
+                                   1 if kind == nat.ROW else t.stride(0))
+    return ep
+
+
+def _run(a, b, c, **kw):
+    print(f"case: A{tuple(a.shape)} B{tuple(b.shape)} C{tuple(c.shape)} {c.dtype} {kw}", flush=True)
+    args = nat.gemm_args(a, b, c, **{k: v for k, v in kw.items() if k != "ep"}, ep=kw.get("ep"))
+    nat.run(args, a.device)
+    torch.cuda.synchronize()
+
+
+TILES = [(256, 256), (128, 256), (64, 256), (128, 128), (256, 128)]
+
+
+@pytest.mark.parametrize("tile", TILES, ids=[f"{m}x{n}" for m, n in TILES])
+@pytest.mark.parametrize("shape", [(300, 512, 256), (1, 256, 128), (257, 1000, 640)])
+def test_tile_plain_bf16(tile, shape):
+    m, n, k = shape
+    a, b = _data(m, n, k)
+    ref = O.gemm_fp32(a, b)
+    c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1])
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+def test_tile_bias_gelu_and_split(splits):
+    m, n, k = 200, 1408, 640
+    a, b = _data(m, n, k, seed=1)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias_gelu", O.gemm_fp32(a, b), bias=bias)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    ep = _fused([(bd, nat.ROW)], act=nat.ACT_GELU_TANH, ra=0)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256, splits=splits,
+         ep=ep)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+def test_tile_nothing_past_m():
+    m, n, k = 100, 512, 256
+    a, b = _data(m, n, k, seed=2)
+    room = torch.full((108, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), b.to(DEV), room[:m], kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256)
+    O.assert_close(room[:m], O.gemm_fp32(a, b), rtol=1e-2, atol=1e-2)
+    assert torch.equal(room[m:].cpu(), torch.full((8, n), 7.0, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("out", [torch.float32, torch.float16])
+def test_tile_out_dtypes_residual_colscale(out):
+    m, n, k = 300, 768, 512
+    a, b = _data(m, n, k, seed=3)
+    g = torch.Generator().manual_seed(9)
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    rs = torch.rand(m, 1, generator=g) + 0.5
+    ref = (O.gemm_fp32(a, b) * rs + res.float())
+    c = torch.empty((m, n), dtype=out, device=DEV)
+    resd, rsd = res.to(DEV), rs.to(DEV)
+    ep = _fused([(rsd, nat.COL), (resd, nat.TILE)], cs=0, ta=1)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, ep=ep)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("tile", [(256, 256), (64, 256), (128, 128)])
+def test_tile_fp8_scaled(tile):
+    m, n, k = 300, 512, 1024
+    g = torch.Generator().manual_seed(11)
+    a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    sa = (torch.rand(m, 1, generator=g) * 1.5 + 0.5) / 448
+    sb = (torch.rand(n, generator=g) * 1.5 + 0.5) / 448
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    ref = O.scaled_mm(a8, b8, sa, sb)
+    c = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
+    ep = _fused([(sad, nat.COL), (sbd, nat.ROW)], cs=0, rs=1)
+    _run(a8.to(DEV), b8.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1], ep=ep)
+    assert O.rel_to_max(c.cpu(), ref) < 1e-5
+    # with the bias, into bf16
+    c2 = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    ep = _fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)], cs=0, rs=1, ra=2)
+    _run(a8.to(DEV), b8.to(DEV), c2, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1], ep=ep)
+    O.assert_close(c2, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 32])
+@pytest.mark.parametrize("cfg", [(8, 16, 1), (4, 32, 1), (16, 16, 4), (8, 32, 2)])
+def test_decode(m, cfg):
+    waves, rows, splits = cfg
+    n, k = 1536, 2048
+    a, b = _data(m, n, k, seed=4)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias", O.gemm_fp32(a, b), bias=bias)
+    c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, decode_waves=waves,
+         decode_rows=rows, splits=splits, ep=_fused([(bd, nat.ROW)], ra=0))
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("kernel", ["tile", "tile_split", "decode", "decode_split", "tile_fp32"])
+def test_silu_and_mul(kernel):
+    m = 5 if kernel.startswith("decode") else 300
+    n, k = 768, 512
+    a, b = _data(m, 2 * n, k, seed=7)
+    acc = O.gemm_fp32(a, b)
+    ref = O.silu_and_mul(acc[:, :n], acc[:, n:])
+    dt = torch.float32 if kernel == "tile_fp32" else torch.bfloat16
+    c = torch.empty((m, n), dtype=dt, device=DEV)
+    ep = nat.HkxEpilogue()
+    ep.form = nat.EP_SILU_MUL
+    kw = dict(ep=ep, splits=2 if kernel.endswith("split") else 1)
+    if kernel.startswith("decode"):
+        kw.update(kernel=nat.KERNEL_DECODE, decode_rows=32)
+    else:
+        kw.update(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256)
+    _run(a.to(DEV), b.to(DEV), c, **kw)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+def test_program_pass():
+    """An epilogue outside the fused form: (acc + bias) * 0.5 + gelu(acc * t), cols >= 300
+    set to 0 -- through the register program."""
+    m, n, k = 130, 512, 256
+    a, b = _data(m, n, k, seed=8)
+    g = torch.Generator().manual_seed(10)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    t = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    acc = O.gemm_fp32(a, b)
+    ref = (acc + bias.float()) * 0.5 + O.gelu_tanh(acc * t.float())
+    ref[:, 300:] = 0
+    bd, td = bias.to(DEV), t.to(DEV)
+    ep = nat.HkxEpilogue()
+    ep.form = nat.EP_PROGRAM
+    ep.nops = 2
+    ep.ops[0] = nat.HkxOperand(bd.data_ptr(), nat.ROW, nat.BF16, 1)
+    ep.ops[1] = nat.HkxOperand(td.data_ptr(), nat.TILE, nat.BF16, n)
+    P = nat.OP
+    prog = [("LOAD", 1, 0, 0, 0, 0.0), ("ADD", 1, 0, 1, 0, 0.0), ("CONST", 2, 0, 0, 0, 0.5),
+            ("MUL", 1, 1, 2, 0, 0.0), ("LOAD", 2, 1, 0, 0, 0.0), ("MUL", 2, 0, 2, 0, 0.0),
+            ("GELU", 2, 2, 0, 0, 0.0), ("ADD", 1, 1, 2, 0, 0.0),
+            ("CONST", 3, 0, 0, 0, 300.0), ("COL", 4, 0, 0, 0, 0.0), ("SUB", 3, 3, 4, 0, 0.0),
+            ("CONST", 5, 0, 0, 0, 0.0), ("SELLE", 1, 3, 5, 1, 0.0)]
+    for i, (op, d, x, y, z, imm) in enumerate(prog):
+        ep.ins[i] = nat.HkxInstr(P[op], d, x, y, z, 0, 0, 0, imm)
+    ep.nins, ep.out_reg = len(prog), 1
+    for kw in (dict(kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256),
+               dict(kernel=nat.KERNEL_TILE, tile_m=64, tile_n=256, splits=2)):
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=ep, **kw)
+        O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+def test_quantizing_stores():
+    m, n, k = 128, 512, 512
+    a, b = _data(m, n, k, seed=12)
+    acc = O.gemm_fp32(a, b)
+    s = torch.full((n,), 40.0)
+    sd = s.to(DEV)
+    c = torch.empty((m, n), dtype=torch.int8, device=DEV)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256,
+         ep=_fused([(sd, nat.ROW)], rs=0))
+    assert (c.cpu().float() - O.quantize_int8(acc * 40)).abs().max().item() <= 1.0
+    c8 = torch.empty((m, n), dtype=torch.float8_e4m3fn, device=DEV)
+    s2 = torch.rand(n, generator=torch.Generator().manual_seed(3)) * 900
+    s2d = s2.to(DEV)
+    _run(a.to(DEV), b.to(DEV), c8, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256,
+         ep=_fused([(s2d, nat.ROW)], rs=0))
+    want = (acc * s2).clamp(-448, 448)
+    got = c8.cpu().float()
+    big = want.abs() > 16
+    assert ((got - want).abs() / want.abs())[big].max().item() < 0.07
+    assert got.abs().max().item() == 448.0
