@@ -23,6 +23,8 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 OUT = HERE / "hk" / "_lib"
 LIB = OUT / "libhkx.so"
+PROBE_SRC = HERE / "probes" / "peaks.hip"
+PROBE_LIB = OUT / "libhkx_probe.so"
 ARCH = "gfx950"
 
 FLAGS = [
@@ -82,6 +84,12 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
     os.replace(tmp, LIB)
+    # the measured-ceilings probe (bench.py reports roofline fractions against it too)
+    r = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-shared", "-fPIC",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                        "-o", str(PROBE_LIB), str(PROBE_SRC)], capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"probe build failed:\n{r.stderr[-4000:]}")
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
     return LIB

@@ -47,6 +47,8 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 struct Plan {
   int kernel;     // HKX_KERNEL_TILE / _DECODE
   int tile_m, tile_n, wm;
+  int tile_waves;  // 4: tile4_kernel, 8: tile_kernel
+  int variant;
   int waves, fn, mf;  // decode
   int splits;     // effective (no empty split)
   int kunits;     // TILE: 128-byte K stages; DECODE: 128-element K groups
@@ -197,6 +199,13 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     p->tile_m = bm;
     p->tile_n = bn;
     p->wm = wave_rows(bm, bn);
+    const bool four_ok = bn == 256 && (bm == 256 || bm == 128 || bm == 64);
+    p->tile_waves = a->tile_waves ? a->tile_waves : (four_ok ? 4 : 8);
+    p->variant = a->variant;
+    if (p->tile_waves != 4 && p->tile_waves != 8)
+      return fail(HKX_ERR_ARG, "tile_waves %d: 4 or 8", a->tile_waves);
+    if (p->tile_waves == 4 && !four_ok)
+      return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
     p->kunits = a->k * eb / 128;
   } else if (kernel == HKX_KERNEL_DECODE) {
     if (a->ab_dtype != HKX_BF16) return fail(HKX_ERR_DTYPE, "the decode kernel takes bf16");
@@ -266,6 +275,11 @@ int launched(hipError_t e, const char* what) {
 hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mode, dim3 grid,
                          hipStream_t s) {
   const int bm = p.tile_m, bn = p.tile_n;
+  if (p.tile_waves == 4) {
+    if (bm == 256) return hkx::launch_tile4<256, 256>(t, fp8, mode, p.variant, grid, s);
+    if (bm == 128) return hkx::launch_tile4<128, 256>(t, fp8, mode, p.variant, grid, s);
+    return hkx::launch_tile4<64, 256>(t, fp8, mode, p.variant, grid, s);
+  }
   if (bm == 256 && bn == 256) return hkx::launch_tile<256, 256, 2>(t, fp8, mode, grid, s);
   if (bm == 128 && bn == 256) return hkx::launch_tile<128, 256, 2>(t, fp8, mode, grid, s);
   if (bm == 64 && bn == 256) return hkx::launch_tile<64, 256, 1>(t, fp8, mode, grid, s);

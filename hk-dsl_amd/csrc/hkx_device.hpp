@@ -41,6 +41,13 @@ HKX_DEV i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
   return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
 }
 
+// 16 bytes a lane from global memory straight into LDS: lane l's bytes land at
+// lds + 16 l (the LDS base is wave-uniform; it goes in M0).
+HKX_DEV void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voff, soff, 0, 0);
+}
+
 // ---------------------------------------------------------------- conversions
 
 HKX_DEV float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }

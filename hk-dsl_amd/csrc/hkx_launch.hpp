@@ -8,11 +8,16 @@
 #include "hkx_decode.hpp"
 #include "hkx_reduce.hpp"
 #include "hkx_tile.hpp"
+#include "hkx_tile4.hpp"
 
 namespace hkx {
 
 template <int BM, int BN, int WM>
 hipError_t launch_tile(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
+
+template <int BM, int BN>
+hipError_t launch_tile4(const TileArgs& a, bool fp8, int mode, int variant, dim3 grid,
+                        hipStream_t s);
 
 hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
                          hipStream_t s);
@@ -39,6 +44,37 @@ hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool progra
         case kStoreF32: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kStoreF32>), grid, block, 0, s, a); break; \
         case kPair16: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kPair16>), grid, block, 0, s, a); break;     \
         case kPairWs: hipLaunchKernelGGL((tile_kernel<BM, BN, WM, false, kPairWs>), grid, block, 0, s, a); break;     \
+        default: return hipErrorInvalidValue;                                                \
+      }                                                                                      \
+    }                                                                                        \
+    return hipGetLastError();                                                                \
+  }
+
+#define HKX_TILE4_LAUNCHER(BM, BN)                                                           \
+  template <>                                                                                \
+  hipError_t launch_tile4<BM, BN>(const TileArgs& a, bool fp8, int mode, int variant,        \
+                                  dim3 grid, hipStream_t s) {                                \
+    const dim3 block(256);                                                                   \
+    if (variant == 1) { /* the compiler's own K-loop schedule, for comparison */            \
+      if (mode != kStore16) return hipErrorInvalidValue;                                     \
+      if (fp8) hipLaunchKernelGGL((tile4_kernel<BM, BN, true, kStore16, 0>), grid, block, 0, s, a); \
+      else hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kStore16, 0>), grid, block, 0, s, a);    \
+      return hipGetLastError();                                                              \
+    }                                                                                        \
+    if (fp8) {                                                                               \
+      switch (mode) {                                                                        \
+        case kStore16: hipLaunchKernelGGL((tile4_kernel<BM, BN, true, kStore16>), grid, block, 0, s, a); break;   \
+        case kStore8: hipLaunchKernelGGL((tile4_kernel<BM, BN, true, kStore8>), grid, block, 0, s, a); break;     \
+        case kStoreF32: hipLaunchKernelGGL((tile4_kernel<BM, BN, true, kStoreF32>), grid, block, 0, s, a); break; \
+        default: return hipErrorInvalidValue;                                                \
+      }                                                                                      \
+    } else {                                                                                 \
+      switch (mode) {                                                                        \
+        case kStore16: hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kStore16>), grid, block, 0, s, a); break;   \
+        case kStore8: hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kStore8>), grid, block, 0, s, a); break;     \
+        case kStoreF32: hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kStoreF32>), grid, block, 0, s, a); break; \
+        case kPair16: hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kPair16>), grid, block, 0, s, a); break;     \
+        case kPairWs: hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kPairWs>), grid, block, 0, s, a); break;     \
         default: return hipErrorInvalidValue;                                                \
       }                                                                                      \
     }                                                                                        \

@@ -58,7 +58,8 @@ class HkxGemmArgs(Structure):
                 ("ldb", c_int64), ("ldc", c_int64), ("m", c_int32), ("n", c_int32),
                 ("k", c_int32), ("ab_dtype", c_int32), ("c_dtype", c_int32),
                 ("kernel", c_int32), ("tile_m", c_int32), ("tile_n", c_int32),
-                ("splits", c_int32), ("decode_waves", c_int32), ("decode_rows", c_int32),
+                ("splits", c_int32), ("tile_waves", c_int32), ("variant", c_int32),
+                ("decode_waves", c_int32), ("decode_rows", c_int32),
                 ("ws", c_void_p), ("ws_bytes", c_size_t), ("ep", HkxEpilogue)]
 
 
@@ -162,8 +163,8 @@ def workspace(device, nbytes: int):
     return buf
 
 
-def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, decode_waves=0,
-              decode_rows=0, ep: HkxEpilogue = None) -> HkxGemmArgs:
+def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, tile_waves=0,
+              variant=0, decode_waves=0, decode_rows=0, ep: HkxEpilogue = None) -> HkxGemmArgs:
     """HkxGemmArgs for A (M, K), B (N, K) -- (2N, K) paired -- and C (M, N) tensors."""
     args = HkxGemmArgs()
     args.a, args.b, args.c = a.data_ptr(), b.data_ptr(), c.data_ptr()
@@ -173,6 +174,7 @@ def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, deco
     args.ab_dtype = dtype_code(a.dtype)
     args.c_dtype = dtype_code(c.dtype)
     args.kernel, args.tile_m, args.tile_n, args.splits = kernel, tile_m, tile_n, splits
+    args.tile_waves, args.variant = tile_waves, variant
     args.decode_waves, args.decode_rows = decode_waves, decode_rows
     if ep is not None:
         args.ep = ep

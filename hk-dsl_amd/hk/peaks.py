@@ -1,0 +1,102 @@
+"""This GPU's measured ceilings: the MFMA rate of a register-only loop, the HBM read
+rate past the 256 MB Infinity Cache, and the shader clock under MFMA load -- the
+measured side of every roofline fraction (the datasheet side is hk.target.CEILINGS).
+The reference measures the same three (tools/cdna-probes/peaks.hip:1-17,
+docs/history/42-mi355x-in-the-engine.md:17-22)."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+_LIB = None
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        import torch  # noqa: F401,PLC0415
+
+        path = Path(__file__).resolve().parent / "_lib" / "libhkx_probe.so"
+        if not path.is_file():
+            raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
+        _LIB = ctypes.CDLL(str(path))
+        for f in ("hkxp_mfma", "hkxp_read", "hkxp_clock"):
+            getattr(_LIB, f).restype = ctypes.c_int
+    return _LIB
+
+
+def _time(fn, reps=5):
+    import torch  # noqa: PLC0415
+
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(reps):
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e) * 1e-3)
+    return best
+
+
+def mfma_tflops(fp8: bool = False, device="cuda:0") -> float:
+    """Dense MFMA TFLOP/s of 4 independent 32x32 chains a wave, 4 waves a CU x 256 CUs
+    (bf16 v_mfma_f32_32x32x16_bf16, fp8 v_mfma_f32_32x32x64_f8f6f4)."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks, iters = cus * 4, 4000
+    out = torch.zeros(blocks, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    t = _time(lambda: L.hkxp_mfma(int(fp8), blocks, iters, ctypes.c_void_p(out.data_ptr()),
+                                  ctypes.c_void_p(st)))
+    flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
+    return blocks * 4 * iters * 4 * flops_per / t / 1e12
+
+
+def hbm_read_gbs(nbytes: int = 2 << 30, device="cuda:0") -> float:
+    """GB/s of one pass of 16-byte non-temporal reads over `nbytes` (> the 256 MB MALL)."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+    out = torch.zeros(1, dtype=torch.int32, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    t = _time(lambda: L.hkxp_read(ctypes.c_void_p(buf.data_ptr()), ctypes.c_size_t(nbytes),
+                                  ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)))
+    del buf
+    return nbytes / t / 1e9
+
+
+def shader_clock_ghz(device="cuda:0") -> float:
+    """The shader clock under a full-chip MFMA load: s_memtime ticks over the 100 MHz
+    s_memrealtime counter, median over workgroups."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks = cus * 4
+    out = torch.zeros(2 * blocks, dtype=torch.int64, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    L.hkxp_clock(ctypes.c_void_p(out.data_ptr()), blocks, 20000, ctypes.c_void_p(st))
+    torch.cuda.synchronize()
+    v = out.view(blocks, 2).double().cpu()
+    ratio = (v[:, 0] / v[:, 1].clamp_min(1)).median().item()
+    return ratio * 0.1
+
+
+def measure(device="cuda:0") -> dict:
+    return {"mfma_bf16_tflops": mfma_tflops(False, device),
+            "mfma_fp8_tflops": mfma_tflops(True, device),
+            "hbm_read_gbs": hbm_read_gbs(device=device),
+            "shader_clock_ghz_mfma_load": shader_clock_ghz(device)}
+
+
+if __name__ == "__main__":
+    import json
+
+    print(json.dumps(measure()))

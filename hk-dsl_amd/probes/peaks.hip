@@ -1,0 +1,92 @@
+// Measured ceilings of this GPU, the denominators the roofline fractions are also
+// reported against (the reference measures its own the same way: a register-only MFMA
+// loop and an HBM read past the Infinity Cache -- tools/cdna-probes/peaks.hip:1-17).
+//
+//   hkxp_mfma(dtype, waves_per_cu, iters, stream) -> launches the MFMA loop
+//   hkxp_read(ptr, bytes, out, stream)            -> launches the HBM read
+//   hkxp_clock(out, iters, stream)                -> shader clock ticks vs the 100 MHz
+//                                                    real-time counter, under MFMA load
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 4 independent 32x32 accumulators a wave, operands in registers: the MFMA pipe's rate.
+template <bool FP8>
+__global__ void __launch_bounds__(256) mfma_loop(float* out, int iters) {
+  f32x16 acc[4] = {};
+  const int l = threadIdx.x;
+  bf16x8 a = {(__bf16)(l * 1e-3f), (__bf16)1.f, (__bf16)0.5f, (__bf16)0.25f, (__bf16)1.f,
+              (__bf16)2.f, (__bf16)3.f, (__bf16)4.f};
+  i32x8 f = {l, 1, 2, 3, 4, 5, 6, 7};
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (FP8)
+        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f, f, acc[j], 0, 0, 0, 0, 0, 0);
+      else
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, acc[j], 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += acc[j][0] + acc[j][15];
+  if (s == 1234.5f) out[blockIdx.x] = s;  // keeps the loop alive
+}
+
+__global__ void __launch_bounds__(256) read_kernel(const i32x4* p, size_t n16, int* out) {
+  i32x4 acc = {0, 0, 0, 0};
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride * 4) {
+    i32x4 v0 = __builtin_nontemporal_load(p + i);
+    i32x4 v1 = i + stride < n16 ? __builtin_nontemporal_load(p + i + stride) : i32x4{0, 0, 0, 0};
+    i32x4 v2 = i + 2 * stride < n16 ? __builtin_nontemporal_load(p + i + 2 * stride) : i32x4{0, 0, 0, 0};
+    i32x4 v3 = i + 3 * stride < n16 ? __builtin_nontemporal_load(p + i + 3 * stride) : i32x4{0, 0, 0, 0};
+    acc ^= v0 ^ v1 ^ v2 ^ v3;
+  }
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x12345678) out[0] = 1;
+}
+
+__global__ void __launch_bounds__(256) clock_kernel(unsigned long long* out, int iters) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  f32x16 acc[4] = {};
+  bf16x8 a = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+              (__bf16)1.f, (__bf16)1.f};
+  for (int i = 0; i < iters; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, acc[j], 0, 0, 0);
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = t1 - t0;
+    out[2 * blockIdx.x + 1] = r1 - r0;
+  }
+  if (acc[0][0] == 1234.5f) out[0] = 0;
+}
+
+extern "C" {
+
+int hkxp_mfma(int fp8, int blocks, int iters, float* out, void* stream) {
+  if (fp8)
+    hipLaunchKernelGGL(mfma_loop<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  else
+    hipLaunchKernelGGL(mfma_loop<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
+
+int hkxp_read(const void* p, size_t bytes, int* out, void* stream) {
+  hipLaunchKernelGGL(read_kernel, dim3(256 * 16), dim3(256), 0, (hipStream_t)stream,
+                     (const i32x4*)p, bytes / 16, out);
+  return (int)hipGetLastError();
+}
+
+int hkxp_clock(unsigned long long* out, int blocks, int iters, void* stream) {
+  hipLaunchKernelGGL(clock_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -155,6 +155,9 @@ typedef struct HkxGemmArgs {
   int32_t tile_m;   /* TILE: 64, 128 or 256 */
   int32_t tile_n;   /* TILE: 128 or 256 */
   int32_t splits;   /* >= 1; > 1 stores fp32 shares to ws and sums them in order */
+  int32_t tile_waves; /* TILE: 4 (2 x 2 waves, 32 x 32 MFMAs; tile_n 256 only) or 8; 0 = 4
+                         where the tile takes it */
+  int32_t variant;  /* TILE: schedule variant of the K loop, 0 = the default (for tuning) */
   int32_t decode_waves; /* DECODE: waves per workgroup (4, 8 or 16); 0 = default */
   int32_t decode_rows;  /* DECODE: W rows per workgroup (16 or 32); 0 = default */
   void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */
