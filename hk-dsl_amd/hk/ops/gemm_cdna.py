@@ -1,0 +1,149 @@
+"""The gfx950 GEMM route: which of libhkx.so's kernels an M x N x K call runs.
+
+The reference's `gemm_cdna.route` (python/hk/ops/gemm_cdna.py:969-999) answers from a
+measured table (the nearest M on a log scale for that N x K), else a rule (decode for
+M <= 32, small blocks to M 2048, the 256 x 256 pingpong above). This is the same
+contract over this build's kernels:
+
+* `CANDIDATES` -- the schedules a route may name: the 4-wave 32x32-MFMA tile kernel at
+  256 / 128 / 64 rows, the 8-wave 16x16-MFMA one, their split-K forms, the decode kernel;
+* `route(m, n, k)` -- a user record (`OVERRIDE`), else the measured table
+  `hk/tuned/routes_gemm_gfx950.json` (this build's own measurements), else `rule`;
+* `resolve` -- a candidate made concrete for a shape (the decode kernel's split);
+* `fits` -- whether a candidate takes a shape;
+* `matmul` -- the plain bf16 GEMM through it (hk.ops.matmul's gfx950 form).
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+from pathlib import Path
+from typing import Any, Dict, Optional
+
+#: Multiples the kernels need: K in 128-byte stages (64 bf16), N in 4s.
+K_STEP = 64
+BLOCK_N_MIN = 4
+#: CUs of an MI355X.
+CUS = 256
+
+CANDIDATES: Dict[str, Dict[str, Any]] = {
+    "t256": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 4},
+    "t128": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4},
+    "t64": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4},
+    "t256w8": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 8},
+    "t128w8": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 8},
+    "t64w8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 8},
+    "t128n128": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "waves": 8},
+    "t256n128": {"kernel": "tile", "tile_m": 256, "tile_n": 128, "waves": 8},
+    "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 4, "splits": 2},
+    "t128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4, "splits": 2},
+    "t128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4, "splits": 4},
+    "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 2},
+    "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 4},
+    "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 8},
+    "decode": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto"},
+    "decode_w4": {"kernel": "decode", "waves": 4, "rows": 16, "splits": "auto"},
+    "decode_w16": {"kernel": "decode", "waves": 16, "rows": 16, "splits": "auto"},
+}
+
+#: A user's choice laid over everything: {(m, n, k): candidate} or {"*": candidate}.
+OVERRIDE: Dict[Any, str] = {}
+
+TABLE_PATH = Path(__file__).resolve().parents[1] / "tuned" / "routes_gemm_gfx950.json"
+_TABLE: list = []
+
+
+def table() -> Dict[str, Dict[str, str]]:
+    """The measured table: {"NxK": {"M": candidate}} ($HK_GEMM_ROUTES names another)."""
+    if not _TABLE:
+        path = Path(os.environ.get("HK_GEMM_ROUTES", TABLE_PATH))
+        shapes = {}
+        if path.is_file():
+            shapes = json.loads(path.read_text()).get("shapes", {})
+        _TABLE.append(shapes)
+    return _TABLE[0]
+
+
+def fits(name: str, m: int, n: int, k: int, fp8: bool = False) -> bool:
+    """Whether candidate `name` takes an M x N x K call."""
+    c = CANDIDATES.get(name)
+    if c is None or m < 1 or n % BLOCK_N_MIN:
+        return False
+    kstep = 128 if fp8 else 64
+    if k % kstep:
+        return False
+    if c["kernel"] == "decode":
+        return not fp8 and m <= 32 and k % 128 == 0
+    return True
+
+
+def rule(m: int, n: int, k: int, fp8: bool = False) -> str:
+    """The route when no record or table entry names one: the decode kernel at M <= 32
+    (bf16), else the largest tile that still fills the GPU, split over K when even the
+    smallest does not."""
+    if not fp8 and m <= 32 and k % 128 == 0:
+        return "decode"
+    kunits = k * (1 if fp8 else 2) // 128
+
+    def tiles(bm):
+        return math.ceil(m / bm) * math.ceil(n / 256)
+
+    for name, bm in (("t256", 256), ("t128", 128)):
+        if m > bm // 2 and tiles(bm) >= 0.75 * CUS:
+            return name
+    bm = 64 if m <= 64 else (128 if m <= 128 or tiles(128) < 0.75 * CUS else 256)
+    base = {64: "t64", 128: "t128", 256: "t256"}[bm]
+    t = tiles(bm)
+    splits = 1
+    while t * splits * 2 <= 2 * CUS and kunits // (splits * 2) >= 8 and splits < 8:
+        splits *= 2
+    if splits == 1:
+        return base
+    name = f"{base}k{splits}"
+    return name if name in CANDIDATES else base
+
+
+def route(m: int, n: int, k: int, fp8: bool = False) -> str:
+    """The candidate an M x N x K call runs: a user record, else the measured table's
+    nearest M (log scale) for this N x K, else `rule` (gemm_cdna.py:969-999)."""
+    for key in ((m, n, k), "*"):
+        if key in OVERRIDE and fits(OVERRIDE[key], m, n, k, fp8):
+            return OVERRIDE[key]
+    if not fp8:
+        ent = table().get(f"{n}x{k}")
+        if ent:
+            ms = sorted(int(x) for x in ent)
+            best = min(ms, key=lambda x: abs(math.log(x) - math.log(m)))
+            name = ent[str(best)]
+            if fits(name, m, n, k, fp8):
+                return name
+    return rule(m, n, k, fp8)
+
+
+def resolve(rec: Dict[str, Any], m: int, n: int, k: int, fp8: bool = False) -> Dict[str, Any]:
+    """A candidate made concrete for a shape: the decode kernel's split over K (enough
+    workgroups for twice the CUs, at least four 128-element groups a split)."""
+    rec = dict(rec)
+    if rec["kernel"] == "decode" and rec.get("splits") == "auto":
+        wgs = math.ceil(n / (16 * (rec.get("rows", 16) // 16)))
+        groups = k // 128
+        splits = 1
+        while wgs * splits < 2 * CUS and groups // (splits * 2) >= 4:
+            splits *= 2
+        rec["splits"] = splits
+    rec.setdefault("splits", 1)
+    return rec
+
+
+def matmul(a, b, out=None):
+    """C = A @ B^T in bf16 (hk.ops.matmul's gfx950 form, gemm_cdna.py:1090): the
+    template with no epilogue."""
+    from ..templates import gemm as T  # noqa: PLC0415
+
+    return T.gemm(a, b, out=out)
+
+
+__all__ = ["CANDIDATES", "OVERRIDE", "route", "rule", "resolve", "fits", "matmul", "table",
+           "K_STEP", "BLOCK_N_MIN", "CUS"]
