@@ -1,0 +1,220 @@
+"""Benchmark of the GEMM-with-fused-epilogue path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--copy-probe]
+
+A step is one call of hk.templates.gemm on BASELINE.json's config 2 -- the workload its
+metric is quoted on: x bf16[4096, 4096] ~N(0,1), w bf16[4096 (K), 12288 (N)] ~N(0, 0.02)
+(handed to the GEMM once, untimed, as w.t().contiguous(): F.linear's (N, K)), b
+bf16[12288] ~N(0, 0.1); y = gelu_tanh(x @ w + b), fp32 accumulate. Synthetic data,
+resident in HBM before the timed region.
+
+Prints ONE JSON line: the metric and its value (whole-job TFLOP/s), the roofline of the
+dominant kernel (achieved TFLOP/s from HIP events around each launch, against the
+2.5 PFLOP/s bf16 dense peak), the CPU baseline (the oracle, torch fp32 on the host
+cores, on a bounded sample), and, under "also", the other BASELINE configs measured the
+same way: the fused gate_up + silu_and_mul GEMM, the decode GEMMs (HBM GB/s of W, with
+weight copies rotated past the 256 MB Infinity Cache) and the fp8 scaled GEMM.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "hk-dsl_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "TFLOP/s & % MFMA peak (prefill M), HBM GB/s & % peak (decode M≤16)"
+PEAK_BF16, PEAK_FP8, PEAK_HBM = 2500.0, 5000.0, 8000.0
+
+
+def _events_time(fn, steps, warmup):
+    """Average device time of one call (HIP events on the current stream, which the
+    kernels launch on) and the wall time of `steps` calls bracketed by synchronize."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
+    return statistics.mean(per), statistics.median(per), wall
+
+
+def _inputs(m, k, n, seed, dev):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(k, n, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    return x.to(dev), w.t().contiguous().to(dev), b.to(dev)
+
+
+def cpu_baseline(x, wt, b):
+    """The oracle on the host: torch fp32 y = gelu_tanh(x @ w + b) at config 2's full size,
+    median of 3 timed runs after a warm-up (all host threads)."""
+    import torch
+
+    from oracle import gemm_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    xc, wc, bc = x.cpu().float(), wt.cpu().float().t().contiguous(), b.cpu().float()
+    O.linear_bias_gelu(xc[:256], wc, bc)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.linear_bias_gelu(xc, wc, bc)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    m, k = xc.shape
+    n = wc.shape[1]
+    return {"value": round(2 * m * n * k / t / 1e12, 3), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle linear_bias_gelu at the full config-2 size {m}x{k}x{n} (fp32), "
+                      f"median of 3 runs, {t:.2f} s each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="config 2 only, no CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 1 GiB device copy (the scale of rocprof's FETCH/WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not measured "
+              f"(the GEMM shards over M or N with no exchange, or over K with one all-reduce "
+              f"before the epilogue -- see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import hk
+
+    dev = "cuda:0"
+    T = hk.templates.gemm
+    m, k, n = 4096, 4096, 12288
+    x, wt, b = _inputs(m, k, n, 0, dev)
+    out = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    step = lambda: T(x, wt, epilogue=T.bias_gelu, bias=b, out=out)  # noqa: E731
+    # parity first: the measured arm is checked against the fp32 reference
+    ref = torch.nn.functional.gelu(x.float() @ wt.float().t() + b.float(), approximate="tanh")
+    step()
+    torch.testing.assert_close(out.float(), ref, rtol=1e-2, atol=1e-2)
+    del ref
+    flops = 2.0 * m * n * k
+    mean_s, med_s, wall = _events_time(step, args.steps, args.warmup)
+    value = flops * args.steps / wall / 1e12
+    achieved = flops / mean_s / 1e12
+    plan = T.plan(m, n, k)
+    res = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded ~N(0,1) x, ~N(0,0.02) w, ~N(0,0.1) b; resident in HBM)",
+        "config": {"workload": "config 2: bias+gelu_tanh, x bf16[4096,4096] @ w bf16[4096,12288] + b",
+                   "M": m, "N": n, "K": k, "epilogue": "bias_gelu (fused in registers)",
+                   "route": plan[0].route, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
+                     "kernel": "hkx::tile4_kernel<256,256,bf16,kStore16>",
+                     "avg_launch_us": round(mean_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
+                     "algorithmic_flops_per_launch": flops},
+    }
+    tr = os.path.join(ROOT, "profiles", "traffic_tile_bias_gelu_cfg2.json")
+    if os.path.isfile(tr):
+        with open(tr) as f:
+            res["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if not args.quick:
+        res["also"] = other_configs(args.steps, args.warmup)
+        del x, wt, b, out
+        torch.cuda.empty_cache()
+        res["cpu_baseline"] = cpu_baseline(*_inputs(m, k, n, 0, "cpu"))
+    else:
+        res["cpu_baseline"] = None
+    if args.copy_probe:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_probe_bytes"] = src.numel() * 4
+    print(json.dumps(res), flush=True)
+
+
+def other_configs(steps, warmup):
+    """Configs 3-5, timed as config 2 is (HIP events per launch, mean)."""
+    import torch
+
+    import hk
+
+    T = hk.templates.gemm
+    dev = "cuda:0"
+    out = {}
+    # config 3: fused gate_up + silu_and_mul
+    for m in (2048, 8192):
+        x, wt, _ = _inputs(m, 4096, 24576, 3, dev)
+        y = torch.empty(m, 12288, device=dev, dtype=torch.bfloat16)
+        t, _, _ = _events_time(lambda: T(x, wt, epilogue=T.silu_and_mul, out=y), steps, warmup)
+        fl = 2.0 * m * 24576 * 4096
+        out[f"cfg3_gate_up_silu_mul_M{m}"] = {"TFLOP/s": round(fl / t / 1e12, 1),
+                                              "frac_bf16_peak": round(fl / t / 1e12 / PEAK_BF16, 4),
+                                              "us": round(t * 1e6, 1)}
+        del x, wt, y
+    # config 4: decode, 4 weight copies (403 MB) rotated past the 256 MB MALL
+    ws = [_inputs(1, 4096, 12288, 40 + i, dev)[1] for i in range(4)]
+    bias = _inputs(1, 4096, 12288, 4, dev)[2]
+    for m in (1, 4, 16):
+        x = _inputs(m, 4096, 12288, 4, dev)[0]
+        for epi in ("plain", "bias"):
+            y = torch.empty(m, 12288, device=dev, dtype=torch.bfloat16)
+            i = [0]
+
+            def call():
+                w = ws[i[0] % 4]
+                i[0] += 1
+                if epi == "bias":
+                    T(x, w, epilogue=T.bias, bias=bias, out=y)
+                else:
+                    T(x, w, out=y)
+
+            t, _, _ = _events_time(call, max(steps, 40), warmup)
+            byts = 12288 * 4096 * 2 + m * 4096 * 2 + m * 12288 * 2 + (12288 * 2 if epi == "bias" else 0)
+            out[f"cfg4_decode_M{m}_{epi}"] = {"GB/s": round(byts / t / 1e9, 1),
+                                              "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM, 4),
+                                              "us": round(t * 1e6, 2)}
+    del ws
+    # config 5: fp8 e4m3 scaled GEMM + dequant + bias
+    g = torch.Generator().manual_seed(5)
+    x8 = torch.randn(8192, 4096, generator=g).to(torch.float8_e4m3fn).to(dev)
+    w8 = torch.randn(4096, 4096, generator=g).to(torch.float8_e4m3fn).t().contiguous().to(dev)
+    sa = ((torch.rand(8192, 1, generator=g) * 1.5 + 0.5) / 448).to(dev)
+    sb = ((torch.rand(4096, generator=g) * 1.5 + 0.5) / 448).to(dev)
+    bias = (torch.randn(4096, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    y = torch.empty(8192, 4096, device=dev, dtype=torch.bfloat16)
+    t, _, _ = _events_time(lambda: hk.ops.scaled_mm(x8, w8, sa, sb, bias=bias, out=y), steps, warmup)
+    fl = 2.0 * 8192 * 4096 * 4096
+    out["cfg5_fp8_scaled_dequant_bias"] = {"TFLOP/s": round(fl / t / 1e12, 1),
+                                           "frac_fp8_peak": round(fl / t / 1e12 / PEAK_FP8, 4),
+                                           "us": round(t * 1e6, 1)}
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+"""The engine route on the CPU: RouteTable's semantics, the table file format, route_for's
+decisions, the fallback, and the dispatch rebinding with a stand-in vLLM -- the
+reference's tests/hk/ir/test_vllm_gemm.py:35-343 restated (vLLM is not installed here,
+so its dispatcher and layer are stand-ins, as the reference's tests use)."""
+
+import json
+import sys
+import types
+
+import pytest
+import torch
+
+from hk.integration import engine
+from hk.integration import vllm_gemm as V
+
+TABLE = {"arch": "gfx950", "kind": "vllm_linear",
+         "shapes": {"4096x4096": {"runs": [[1, 16, "hk_decode"], [64, 512, "hk"], [1024, 4096, "hk"]]},
+                    "12288x4096": {"runs": [[1, 32, "hk_decode"], [33, 8192, "hk"]], "above": "fallback"},
+                    "1000x64": {"runs": [[1, 8, "fallback"]]}}}
+
+
+def table():
+    return engine.RouteTable(engine.RouteTable.parse(TABLE), meta={"arch": "gfx950"}, source="t")
+
+
+def test_lookup_inside_between_above_below():
+    t = table()
+    assert t.lookup(1, 4096, 4096) == "hk_decode"
+    assert t.lookup(16, 4096, 4096) == "hk_decode"
+    assert t.lookup(17, 4096, 4096) == "fallback"   # between two runs that disagree
+    assert t.lookup(64, 4096, 4096) == "hk"
+    assert t.lookup(600, 4096, 4096) == "fallback"  # between two runs (same path: still a gap)
+    assert t.lookup(9999, 4096, 4096) == "hk"       # above the last run: its path
+    assert t.lookup(9999, 12288, 4096) == "fallback"  # `above` says otherwise
+    assert t.lookup(5, 5, 5) == "fallback" and (5, 5) in t.misses
+    assert t.routes_any(4096, 4096) and not t.routes_any(1000, 64)
+
+
+def test_overlapping_runs_are_refused_and_a_table_round_trips(tmp_path):
+    with pytest.raises(ValueError, match="overlap"):
+        engine.RouteTable({(1, 1): {"runs": [[1, 8, "hk"], [8, 9, "hk"]]}})
+    t = table()
+    p = tmp_path / "routes.json"
+    p.write_text(json.dumps(t.to_json()))
+    t2 = engine.RouteTable.from_json(p)
+    for m in (1, 16, 17, 64, 600, 9999):
+        assert t2.lookup(m, 4096, 4096) == t.lookup(m, 4096, 4096)
+        assert t2.lookup(m, 12288, 4096) == t.lookup(m, 12288, 4096)
+
+
+def test_shipped_table_env_override(tmp_path, monkeypatch):
+    p = tmp_path / "r.json"
+    p.write_text(json.dumps(TABLE))
+    monkeypatch.setenv("HK_TEST_ROUTES", str(p))
+    t = engine.shipped_table("vllm_linear", "gfx950", "HK_TEST_ROUTES")
+    assert t.lookup(64, 4096, 4096) == "hk"
+    monkeypatch.setenv("HK_TEST_ROUTES", str(tmp_path / "missing.json"))
+    with pytest.raises(FileNotFoundError):
+        engine.shipped_table("vllm_linear", "gfx950", "HK_TEST_ROUTES")
+    bad = dict(TABLE, arch="gfx1100")
+    p.write_text(json.dumps(bad))
+    monkeypatch.setenv("HK_TEST_ROUTES", str(p))
+    with pytest.raises(ValueError, match="gfx1100"):
+        engine.shipped_table("vllm_linear", "gfx950", "HK_TEST_ROUTES")
+
+
+@pytest.fixture
+def routed():
+    V.set_routes(table())
+    yield
+    V.set_routes(None)
+
+
+def test_route_for(routed):
+    assert V.route_for(64, 4096, 4096) == "hk"
+    assert V.route_for(8, 4096, 4096) == "hk_decode"
+    assert V.route_for(17, 4096, 4096) == "fallback"
+    assert V.route_for(64, 4096, 4096, bf16=False) == "fallback"
+    assert V.route_for(64, 4096, 4096, contiguous_weight=False) == "fallback"
+    assert V.route_for(0, 4096, 4096) == "fallback"
+    assert V.route_for(64, 4096, 4096, bias=True) == "hk"  # the bias rides the fused epilogue
+    V.BIAS_FUSED = False
+    try:
+        assert V.route_for(64, 4096, 4096, bias=True) == "fallback"  # the reference's rule
+    finally:
+        V.BIAS_FUSED = True
+    assert V.route_for(9999, 12288, 4096) == "fallback"
+
+
+def test_no_table_routes_nothing():
+    V.set_routes(None)
+    V._TABLE.append(None)
+    try:
+        assert V.route_for(64, 4096, 4096) == "fallback"
+    finally:
+        V._TABLE.clear()
+
+
+def test_cpu_tensors_and_fallback_compute_linear(routed):
+    x = torch.randn(3, 5, 64)
+    w = torch.randn(1000, 64)
+    b = torch.randn(1000)
+    y = V._gemm(None, x, w, b)  # a CPU tensor never leaves torch
+    torch.testing.assert_close(y, torch.nn.functional.linear(x, w, b))
+    V.PATCH.reset()
+    y2 = V.linear(x.bfloat16(), w.bfloat16(), None)  # the table sends (1000, 64) to the fallback
+    assert V.PATCH.stats["fallback"] == 1
+    ref = torch.nn.functional.linear(x.bfloat16().float(), w.bfloat16().float())
+    torch.testing.assert_close(y2.float(), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_dispatch_rebinding_with_a_stand_in_vllm(routed, monkeypatch):
+    """vLLM's `dispatch_unquantized_gemm` is replaced in every vllm module that bound it,
+    by identity, and put back by revert()."""
+    calls = []
+
+    def orig_gemm(layer, x, weight, bias=None):
+        calls.append("orig")
+        return torch.nn.functional.linear(x, weight, bias)
+
+    def orig_dispatch(*args, **kwargs):
+        return orig_gemm
+
+    utils = types.ModuleType("vllm.model_executor.layers.utils")
+    utils.dispatch_unquantized_gemm = orig_dispatch
+    other = types.ModuleType("vllm.model_executor.layers.linear")
+    other.dispatch_unquantized_gemm = orig_dispatch
+    platforms = types.ModuleType("vllm.platforms")
+    platforms.current_platform = types.SimpleNamespace(is_rocm=lambda: True)
+    mods = {"vllm": types.ModuleType("vllm"), "vllm.model_executor": types.ModuleType("vllm.model_executor"),
+            "vllm.model_executor.layers": types.ModuleType("vllm.model_executor.layers"),
+            "vllm.model_executor.layers.utils": utils, "vllm.model_executor.layers.linear": other,
+            "vllm.platforms": platforms}
+    mods["vllm.model_executor.layers"].utils = utils
+    for k, v in mods.items():
+        monkeypatch.setitem(sys.modules, k, v)
+    msg = V.apply()
+    assert "2 rebound" in msg, msg
+    assert utils.dispatch_unquantized_gemm is V.dispatch_unquantized_gemm
+    assert other.dispatch_unquantized_gemm is V.dispatch_unquantized_gemm
+    g = utils.dispatch_unquantized_gemm()
+    layer = types.SimpleNamespace()
+    w = torch.randn(1000, 64)
+    g(layer, torch.randn(2, 64), w)  # a shape the table never routes: vLLM's own GEMM
+    assert calls == ["orig"] and layer._hk_gemm[1] is False
+    assert "2 rebound" in V.revert()
+    assert utils.dispatch_unquantized_gemm is orig_dispatch
+
+
+def test_patch_contracts():
+    with pytest.raises(ValueError, match="says why"):
+        engine.Patch("x::y", ["a"], graph="never")
+    p = engine.Patch("x::z", ["a", "b"])
+    p.count("a")
+    p.count("a")
+    assert p.stats == {"a": 2, "b": 0} and "a 2" in p.summary()
+    assert p.guard(lambda v: v + 1)(1) == 2  # free outside capture
