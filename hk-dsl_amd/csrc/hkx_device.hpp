@@ -187,6 +187,10 @@ HKX_DEV float tanh_f(float x) {
   return 2.0f * sigmoid(2.0f * x) - 1.0f;
 }
 
+// The activation as a template parameter (ACT < 0: chosen at run time, act4 below).
+template <int ACT>
+HKX_DEV f32x4 act4c(int act, f32x4 v);
+
 HKX_DEV f32x4 act4(int act, f32x4 v) {
   if (act == HKX_ACT_GELU_TANH) {
     v.x = gelu_tanh(v.x); v.y = gelu_tanh(v.y); v.z = gelu_tanh(v.z); v.w = gelu_tanh(v.w);
@@ -197,6 +201,12 @@ HKX_DEV f32x4 act4(int act, f32x4 v) {
     v.z = __builtin_fmaxf(v.z, 0.0f); v.w = __builtin_fmaxf(v.w, 0.0f);
   }
   return v;
+}
+
+template <int ACT>
+HKX_DEV f32x4 act4c(int act, f32x4 v) {
+  if constexpr (ACT < 0) return act4(act, v);
+  else return act4(ACT, v);
 }
 
 // ---------------------------------------------------------------- the fused form

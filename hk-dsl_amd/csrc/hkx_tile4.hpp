@@ -27,7 +27,7 @@ namespace hkx {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, bool FP8, int MODE, int SCHED = 1>
+template <int BM, int BN, bool FP8, int MODE, int SCHED = 3, int ACT = -1>
 __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   constexpr int TM = BM / 2, TN = BN / 2;
   constexpr int FM = TM / 32, FN = TN / 32;
@@ -39,7 +39,11 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   constexpr bool PAIR = (MODE == kPair16 || MODE == kPairWs);
   constexpr int OB = (MODE == kStore8) ? 1 : 2;
   constexpr int OUTW = PAIR ? BN / 2 : BN;  // C columns a tile covers
-  constexpr int SMEM = 2 * STAGE;
+  constexpr bool STAGED = (MODE == kStore16 || MODE == kStore8 || MODE == kPair16);
+  constexpr int RS = OUTW * OB + 16;  // staging row stride, bytes
+  constexpr int STAGING = STAGED ? BM * RS : 0;
+  constexpr int ROWOP = (2 * STAGE > STAGING) ? 2 * STAGE : STAGING;  // + the row operands
+  constexpr int SMEM = ROWOP + 2 * BN * 4;
   static_assert(FM >= 1 && FN >= 1 && BM % 64 == 0 && BN == 256, "tiling");
   static_assert(!PAIR || FN % 2 == 0, "the paired form needs gate/up fragment pairs");
   static_assert(SMEM <= 160 * 1024, "LDS");
@@ -93,11 +97,21 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
     }
   }
   auto fill = [&](int kt, int s) {
-    const uint32_t so = (uint32_t)(kt0 + kt) * 128u;
+    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(kt0 + kt) * 128u);
     uint8_t* base = smem + s * STAGE + wave * 1024;
 #pragma unroll
     for (int i = 0; i < NCH; ++i)
       buf_load16_lds(i < NA ? ra : rb, base + i * 4096, voff[i], so);
+  };
+
+  // Fills [lo, hi) of a stage only: the default schedule spreads a stage's fills over
+  // three k-steps.
+  auto fill_part = [&](int kt, int s, int lo, int hi) {
+    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(kt0 + kt) * 128u);
+    uint8_t* base = smem + s * STAGE + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i)
+      if (i >= lo && i < hi) buf_load16_lds(i < NA ? ra : rb, base + i * 4096, voff[i], so);
   };
 
   // ---- fragment reads: lane l reads row l & 31 of a fragment, k-half l >> 5
@@ -159,6 +173,25 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
 
   Frag a0[FM], b0[FN], a1[FM], b1[FN];
 
+  // ---- the epilogue's operands, loaded now, so their latency hides under the K loop:
+  // the row operands (one value per column of the tile) into LDS, fp32, thread t
+  // column n0 + t; the column scale for each of this lane's rows into a register.
+  const Fused& e = p.ep;
+  const bool fused = !PAIR && e.form == HKX_EP_FUSED;
+  float* rowop = (float*)(smem + ROWOP);  // [0, BN): row scale, [BN, 2 BN): row add
+  if (tid < BN) {
+    const int n = n0 + tid;
+    const bool ok = fused && n < p.N;
+    rowop[tid] = (ok && e.rs.p) ? ld1(e.rs.p, e.rs.dt, e.rs.ld ? n : 0) : 1.0f;
+    rowop[BN + tid] = (ok && e.ra.p) ? ld1(e.ra.p, e.ra.dt, e.ra.ld ? n : 0) : 0.0f;
+  }
+  float csv[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * TM + 32 * i + (lane & 31);
+    csv[i] = (fused && e.cs.p && m < p.M) ? ld_col(e.cs, m) * e.cmul : e.cmul;
+  }
+
   // ---- prologue: stages 0 and 1 in flight, stage 0 landed, its first fragments read
   fill(0, 0);
   if (nkt > 1) fill(1, 1);
@@ -166,15 +199,22 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   __syncthreads();
   read_frags(0, 0, a0, b0);
 
-  // One iteration is one 128-byte K stage: KS k-steps of FM x FN MFMAs. The body is one
-  // basic block (the fills and reads past the last stage are kept, pointed at the last
-  // stage again, and never used), so the MFMAs, the fragment reads and the fills can be
-  // interleaved explicitly: SCHED 1 puts one LDS read after each of the first MFMAs of a
-  // step, and in the last step the fills too, so the MFMA pipe is never left waiting on
-  // an issue slot. SCHED 0 leaves the order to the compiler.
+  // One iteration is one 128-byte K stage: KS k-steps of FM x FN MFMAs, fragment reads one
+  // k-step ahead. The body is one basic block (fills and reads past the last stage are
+  // kept, pointed at the last stage again, and never used), so the MFMAs, the reads and
+  // the fills are interleaved by sched_group_barrier:
+  //
+  // * SCHED 3 (the default): the next tile's fills -- into the stage freed at this
+  //   iteration's barrier -- start under the last k-step (3/8 of them) and go on under
+  //   the next iteration's first two k-steps. A burst of fills blocks the wave's
+  //   in-order issue (every wave of the CU issues its 16 at once and they queue at the
+  //   address unit), so spread out they cost a third less; spread over three k-steps
+  //   they still land before the barrier that waits for them.
+  // * SCHED 1: all the fills in one burst under the last k-step (for comparison).
   constexpr int NRD = FP8 ? 2 * (FM + FN) : (FM + FN);  // ds_read_b128 per k-step
   for (int kt = 0; kt < nkt; ++kt) {
     const int s = kt & 1;
+    const int tk = min(kt + 1, nkt - 1);
 #pragma unroll
     for (int ks = 0; ks < KS - 1; ++ks) {
       if (ks & 1) {
@@ -184,134 +224,159 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
         read_frags(s, ks + 1, a1, b1);
         mma(a0, b0);
       }
-      if constexpr (SCHED == 1) {
+      if constexpr (SCHED == 3) {
+        // the rest of tile kt + 1's fills, begun under iteration kt - 1's last k-step
+        constexpr int F0 = NCH * 3 / 8, F1 = NCH * 11 / 16;
+        if (KS == 2) {
+          fill_part(tk, s ^ 1, F0, NCH);
+        } else {
+          if (ks == 0) fill_part(tk, s ^ 1, F0, F1);
+          if (ks == 1) fill_part(tk, s ^ 1, F1, NCH);
+        }
 #pragma unroll
         for (int q = 0; q < NRD; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 fill
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, NCH, 0);
+      } else {
+#pragma unroll
+        for (int q = 0; q < NRD; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
       }
-      if constexpr (SCHED != 0) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // every wave is done reading stage s once this barrier passes (its last reads were
-    // waited for), and stage s ^ 1 -- the next tile, filled since iteration kt - 1 --
-    // has landed: each wave waits for its own fills first (the barrier's fence waits
-    // only for LDS operations, not for these buffer loads)
+    // waited for), and stage s ^ 1 -- the next tile -- has landed: each wave waits for its
+    // own fills first (the barrier's fence waits only for LDS operations, not for these
+    // buffer loads)
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
     __syncthreads();
-    fill(min(kt + 2, nkt - 1), s);
+    if constexpr (SCHED == 3)
+      fill_part(min(kt + 2, nkt - 1), s, 0, NCH * 3 / 8);
+    else
+      fill(min(kt + 2, nkt - 1), s);
     // KS is even: step KS-1 multiplies set 1 while the next stage's step 0 reads set 0
     read_frags(s ^ 1, 0, a0, b0);
     mma(a1, b1);
-    if constexpr (SCHED == 1) {
 #pragma unroll
-      for (int q = 0; q < NRD; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, NCH / NRD, 0);  // fills
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
+    for (int q = 0; q < NRD; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, SCHED == 3 ? 1 : NCH / NRD, 0);
     }
-    if constexpr (SCHED != 0) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, NCH, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   __builtin_amdgcn_s_waitcnt(0x3f70);  // the last (unused) fills land before LDS is reused
 
-  // ---- the store, in FM rounds. Round r parks every wave's fragment row r (fp32, 64
-  // rows x BN columns: rows 32 wm + (l & 31), columns wn TN + 32 j + 8 g + 4 (l >> 5) for
-  // run g) in an LDS slab; then each thread takes 8 consecutive columns of 8 slab rows,
-  // runs the epilogue on them in registers and stores them as one 16-byte (8 x bf16) or
-  // 32-byte (fp32) row piece. The epilogue is a rolled loop, so it costs no code per
-  // accumulator and no registers beside the K loop's.
-  constexpr int SR = BN * 4 + 16;  // slab row stride, bytes
-  static_assert(64 * SR <= 2 * STAGE, "slab");
-  const int orow = tid >> 5;        // slab rows orow + 8 q
-  const int oc8 = (tid & 31) * 8;   // this thread's 8 columns of the slab (BN = 256)
-  float* out32 = (float*)p.c + (int64_t)split * p.split_stride;
-  // The row operands of the fused form depend on the column alone: loaded once.
-  const Fused& e = p.ep;
-  const bool fused = !PAIR && e.form == HKX_EP_FUSED;
-  const int nq = n0 + oc8;
-  const bool hi_ok = nq + 4 < p.N;  // N % 4 == 0: the second run of four is in or out whole
-  f32x4 rs0 = {1.f, 1.f, 1.f, 1.f}, rs1 = rs0, ra0 = {0.f, 0.f, 0.f, 0.f}, ra1 = ra0;
-  if (fused && nq < p.N) {
-    if (e.rs.p) { rs0 = ld_row(e.rs, nq); if (hi_ok) rs1 = ld_row(e.rs, nq + 4); }
-    if (e.ra.p) { ra0 = ld_row(e.ra, nq); if (hi_ok) ra1 = ld_row(e.ra, nq + 4); }
-  }
-#pragma unroll  // acc[r] must be a static index: the accumulators live in AGPRs
-  for (int r = 0; r < FM; ++r) {
-    __syncthreads();  // the K loop's (or the last round's) reads of LDS are done
+  // ---- the store. Lane l holds, for fragment (i, j) and run g, C[m][n .. n + 3] with
+  // m = wm TM + 32 i + (l & 31), n = wn TN + 32 j + 8 g + 4 (l >> 5). The fused epilogue
+  // runs on them in registers; a 16- or 8-bit C is converted once and staged in LDS, then
+  // stored as 16-byte pieces of whole rows (row-contiguous stores cost half of the
+  // scattered 8-byte ones); an fp32 C or the fp32 shares go straight from the registers.
+  const int mw = wm * TM + (lane & 31);
+  const int nw = wn * TN + 4 * h;
+  if constexpr (MODE == kStoreF32 || MODE == kPairWs) {
+    float* out = (float*)p.c + (int64_t)split * p.split_stride;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + mw + 32 * i;
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *(f32x4*)(smem + (wm * 32 + rf) * SR + (wn * TN + 32 * j + 8 * g + 4 * h) * 4) =
-            f32x4{acc[r][j][4 * g], acc[r][j][4 * g + 1], acc[r][j][4 * g + 2],
-                  acc[r][j][4 * g + 3]};
-    __syncthreads();
-    if (PAIR && oc8 >= BN / 2) continue;
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int sr = orow + 8 * q;
-      const int m = m0 + (sr >> 5) * TM + 32 * r + (sr & 31);
-      const uint8_t* src = smem + sr * SR;
-      const int n = nq;
-      if (m >= p.M || n >= p.N) continue;
-      f32x4 v0, v1;
-      if constexpr (PAIR) {
-        // slab columns are fragments: gate in even 32-column blocks, up in odd ones
-        const int vb = (oc8 >> 5) * 64 + (oc8 & 31);
-        const f32x4 g0 = *(const f32x4*)(src + vb * 4), g1 = *(const f32x4*)(src + vb * 4 + 16);
-        const f32x4 u0 = *(const f32x4*)(src + (vb + 32) * 4);
-        const f32x4 u1 = *(const f32x4*)(src + (vb + 32) * 4 + 16);
-        if constexpr (MODE == kPairWs) {
-          float* o = out32 + (int64_t)m * p.ldc;
-          *(f32x4*)(o + n) = g0;
-          *(f32x4*)(o + p.N + n) = u0;
-          if (hi_ok) {
-            *(f32x4*)(o + n + 4) = g1;
-            *(f32x4*)(o + p.N + n + 4) = u1;
+        for (int g = 0; g < 4; ++g) {
+          __builtin_amdgcn_sched_barrier(0);
+          f32x4 v = f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                          acc[i][j][4 * g + 3]};
+          if constexpr (MODE == kStoreF32) {
+            const int n = n0 + nw + 32 * j + 8 * g;
+            if (m < p.M && n < p.N) {
+              if (fused) {
+                const int nl = nw + 32 * j + 8 * g;
+                v = v * (*(const f32x4*)(rowop + nl) * csv[i]) + *(const f32x4*)(rowop + BN + nl);
+                if (e.ta.p) v += ld_tile(e.ta, m, n);
+                v = act4(e.act, v + e.cadd);
+              }
+              *(f32x4*)(out + (int64_t)m * p.ldc + n) = v;
+            }
+          } else {
+            const int fv = wn * FN + j;
+            const int oc = n0 + (fv >> 1) * 32 + 8 * g + 4 * h;
+            if (m < p.M && oc < p.N)
+              *(f32x4*)(out + (int64_t)m * p.ldc + oc + ((fv & 1) ? p.N : 0)) = v;
           }
-          continue;
         }
-        v0 = silu_mul4(g0, u0);
-        v1 = silu_mul4(g1, u1);
+    }
+  } else {
+    __syncthreads();  // the stages are reused as the staging tile
+    // Straight-line code, no branch between the element groups, so the scheduler can
+    // overlap one group's dependent chain (AGPR read, math, convert, LDS write) with the
+    // next's -- with one wave a SIMD nothing else would hide its latency. Absent row and
+    // column operands hold 1 and 0 (the identity); rows past M and columns past N are
+    // computed from clamped, in-bounds loads and never stored.
+    auto group = [&](int i, int j, int g, bool tile_op) {
+      const int ml = mw + 32 * i;
+      f32x4 v = f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                      acc[i][j][4 * g + 3]};
+      int cl;
+      if constexpr (MODE == kPair16) {
+        const f32x4 u = f32x4{acc[i][j + 1][4 * g], acc[i][j + 1][4 * g + 1],
+                              acc[i][j + 1][4 * g + 2], acc[i][j + 1][4 * g + 3]};
+        v = silu_mul4(v, u);
+        cl = ((wn * FN + j) >> 1) * 32 + 8 * g + 4 * h;
       } else {
-        v0 = *(const f32x4*)(src + oc8 * 4);
-        v1 = *(const f32x4*)(src + oc8 * 4 + 16);
-        if (fused) {
-          if (e.cs.p) {
-            const float sc = ld_col(e.cs, m);
-            v0 *= sc;
-            v1 *= sc;
-          }
-          v0 = v0 * rs0 * e.cmul + ra0;
-          v1 = v1 * rs1 * e.cmul + ra1;
-          if (e.ta.p) {
-            v0 += ld_tile(e.ta, m, n);
-            if (hi_ok) v1 += ld_tile(e.ta, m, n + 4);
-          }
-          v0 = act4(e.act, v0 + e.cadd);
-          v1 = act4(e.act, v1 + e.cadd);
+        cl = nw + 32 * j + 8 * g;
+        v = v * (*(const f32x4*)(rowop + cl) * csv[i]) + *(const f32x4*)(rowop + BN + cl);
+        if (tile_op) {
+          const int m = min(m0 + ml, p.M - 1), n = min(n0 + cl, p.N - 4);
+          v += ld_tile(e.ta, m, n);
+        }
+        v = act4c<ACT>(e.act, v + e.cadd);
+      }
+      const u32x2 w = pack4<OB>(p.c_dt, v);
+      if constexpr (OB == 2)
+        *(u32x2*)(smem + ml * RS + cl * 2) = w;
+      else
+        *(uint32_t*)(smem + ml * RS + cl) = w.x;
+    };
+    const bool tile_op = fused && e.ta.p;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if (PAIR && (j & 1)) continue;
+        __builtin_amdgcn_sched_barrier(0);  // a fragment (16 elements) at a time
+        if (tile_op) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) group(i, j, g, true);
+        } else {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) group(i, j, g, false);
         }
       }
-      if constexpr (MODE == kStoreF32) {
-        float* o = out32 + (int64_t)m * p.ldc + n;
-        *(f32x4*)o = v0;
-        if (hi_ok) *(f32x4*)(o + 4) = v1;
-      } else {
-        uint8_t* dst = (uint8_t*)p.c + ((int64_t)m * p.ldc + n) * OB;
-        const u32x2 w0 = pack4<OB>(p.c_dt, v0), w1 = pack4<OB>(p.c_dt, v1);
-        if constexpr (OB == 2) {
-          if (p.c_aligned && hi_ok) {
-            *(i32x4*)dst = i32x4{(int)w0.x, (int)w0.y, (int)w1.x, (int)w1.y};
-          } else {
-            *(u32x2*)dst = w0;
-            if (hi_ok) *(u32x2*)(dst + 8) = w1;
-          }
+    }
+    __syncthreads();
+    constexpr int CPR = OUTW * OB / 16;  // 16-byte chunks a row
+    constexpr int EPC = 16 / OB;         // elements a chunk
+#pragma unroll 4
+    for (int q = tid; q < BM * CPR; q += 256) {
+      const int row = q / CPR, ch = q - row * CPR;
+      const int gmr = m0 + row, gn = n0 + ch * EPC;
+      if (gmr < p.M && gn < p.N) {
+        const uint8_t* src = smem + row * RS + ch * 16;
+        uint8_t* dst = (uint8_t*)p.c + ((int64_t)gmr * p.ldc + gn) * OB;
+        if (p.c_aligned && gn + EPC <= p.N) {
+          *(i32x4*)dst = *(const i32x4*)src;
         } else {
-          *(uint32_t*)dst = w0.x;
-          if (hi_ok) *(uint32_t*)(dst + 4) = w1.x;
+          const int cnt = min(EPC, p.N - gn) * OB;
+          for (int x = 0; x < cnt; ++x) dst[x] = src[x];
         }
       }
     }

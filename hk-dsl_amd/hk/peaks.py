@@ -21,7 +21,7 @@ def _lib():
         if not path.is_file():
             raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
         _LIB = ctypes.CDLL(str(path))
-        for f in ("hkxp_mfma", "hkxp_read", "hkxp_clock"):
+        for f in ("hkxp_mfma", "hkxp_read", "hkxp_clock", "hkxp_lds"):
             getattr(_LIB, f).restype = ctypes.c_int
     return _LIB
 
@@ -89,11 +89,30 @@ def shader_clock_ghz(device="cuda:0") -> float:
     return ratio * 0.1
 
 
+def lds_read_bytes_per_clk(pattern: int = 0, device="cuda:0") -> float:
+    """LDS bytes read per clock per CU by ds_read_b128 (pattern 0: conflict-free lines;
+    1: the GEMM kernels' swizzled fragment reads), at the clock shader_clock_ghz reads."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks, iters = cus * 2, 2000
+    out = torch.zeros(blocks, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    t = _time(lambda: L.hkxp_lds(pattern, blocks, iters, ctypes.c_void_p(out.data_ptr()),
+                                 ctypes.c_void_p(st)))
+    byts = blocks * 256 * 16 * 16 * iters
+    clk = shader_clock_ghz(device) * 1e9
+    return byts / t / cus / clk
+
+
 def measure(device="cuda:0") -> dict:
     return {"mfma_bf16_tflops": mfma_tflops(False, device),
             "mfma_fp8_tflops": mfma_tflops(True, device),
             "hbm_read_gbs": hbm_read_gbs(device=device),
-            "shader_clock_ghz_mfma_load": shader_clock_ghz(device)}
+            "shader_clock_ghz_mfma_load": shader_clock_ghz(device),
+            "lds_read_b128_bytes_per_clk_cu": lds_read_bytes_per_clk(0, device),
+            "lds_read_b128_bytes_per_clk_cu_fragment_pattern": lds_read_bytes_per_clk(1, device)}
 
 
 if __name__ == "__main__":

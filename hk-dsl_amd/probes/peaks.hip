@@ -14,17 +14,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// 4 independent 32x32 accumulators a wave, operands in registers: the MFMA pipe's rate.
-template <bool FP8>
+// CH independent 32x32 accumulators a wave, operands in registers: the MFMA pipe's rate.
+template <bool FP8, int CH = 4>
 __global__ void __launch_bounds__(256) mfma_loop(float* out, int iters) {
-  f32x16 acc[4] = {};
+  f32x16 acc[CH] = {};
   const int l = threadIdx.x;
   bf16x8 a = {(__bf16)(l * 1e-3f), (__bf16)1.f, (__bf16)0.5f, (__bf16)0.25f, (__bf16)1.f,
               (__bf16)2.f, (__bf16)3.f, (__bf16)4.f};
   i32x8 f = {l, 1, 2, 3, 4, 5, 6, 7};
   for (int i = 0; i < iters; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < CH; ++j) {
       if constexpr (FP8)
         acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f, f, acc[j], 0, 0, 0, 0, 0, 0);
       else
@@ -33,7 +33,7 @@ __global__ void __launch_bounds__(256) mfma_loop(float* out, int iters) {
   }
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) s += acc[j][0] + acc[j][15];
+  for (int j = 0; j < CH; ++j) s += acc[j][0] + acc[j][15];
   if (s == 1234.5f) out[blockIdx.x] = s;  // keeps the loop alive
 }
 
@@ -68,7 +68,50 @@ __global__ void __launch_bounds__(256) clock_kernel(unsigned long long* out, int
   if (acc[0][0] == 1234.5f) out[0] = 0;
 }
 
+// LDS read bandwidth: every wave reads 16 bytes a lane per ds_read_b128, `iters` x 16
+// reads. pattern 0: lane l reads bytes 16 l of a 1 KB slab (conflict-free); pattern 1:
+// the GEMM kernels' fragment read, row l & 31 of 128-byte rows, chunk (2 (i & 3) +
+// (l >> 5)) ^ swz(l & 15).
+__global__ void __launch_bounds__(256) lds_read_kernel(float* out, int iters, int pattern) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[65536];
+  const int t = threadIdx.x, l = t & 63, w = t >> 6;
+  for (int i = t; i < 65536 / 16; i += 256) ((i32x4*)lds)[i] = i32x4{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  i32x4 acc = {0, 0, 0, 0};
+  unsigned off[4];
+  for (int q = 0; q < 4; ++q) {
+    if (pattern == 0) {
+      off[q] = (unsigned)(w * 4096 + q * 1024 + l * 16);
+    } else {
+      const int r = l & 31, j = r & 15, sw = (j ^ (j >> 3)) & 7;
+      off[q] = (unsigned)(w * 16384 + r * 128 + (((2 * q + (l >> 5)) ^ sw) << 4));
+    }
+  }
+  for (int it = 0; it < iters; ++it) {
+    unsigned z = (unsigned)(it & 3) << 14;
+    asm volatile("" : "+v"(z));  // an offset the compiler cannot see through: no hoisting
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const i32x4 v = *(const i32x4*)(lds + ((off[q & 3] + ((q >> 2) << 12) + z) & 65535));
+      acc ^= v;
+    }
+  }
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x7777777) out[blockIdx.x] = 1.f;
+}
+
 extern "C" {
+
+int hkxp_lds(int pattern, int blocks, int iters, float* out, void* stream) {
+  hipLaunchKernelGGL(lds_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters,
+                     pattern);
+  return (int)hipGetLastError();
+}
+
+
+int hkxp_mfma16(int blocks, int iters, float* out, void* stream) {
+  hipLaunchKernelGGL((mfma_loop<false, 16>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
 
 int hkxp_mfma(int fp8, int blocks, int iters, float* out, void* stream) {
   if (fp8)
