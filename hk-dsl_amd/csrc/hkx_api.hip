@@ -1,3 +1,4 @@
+#include <algorithm>
 // The C ABI of libhkx.so (include/hkx.h): argument checks, the plan of launches for a
 // call, and the launches on the caller's stream. Stateless and reentrant; the only
 // state is each thread's last error message.
@@ -47,7 +48,7 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 struct Plan {
   int kernel;     // HKX_KERNEL_TILE / _DECODE
   int tile_m, tile_n, wm;
-  int tile_waves;  // 4: tile4_kernel, 8: tile_kernel
+  int schedule;   // HKX_TILE_PINGPONG: pp_kernel, _W4: tile4_kernel, _W8: tile_kernel
   int variant;
   int waves, fn, mf;  // decode
   int splits;     // effective (no empty split)
@@ -200,12 +201,19 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     p->tile_n = bn;
     p->wm = wave_rows(bm, bn);
     const bool four_ok = bn == 256 && (bm == 256 || bm == 128 || bm == 64);
-    p->tile_waves = a->tile_waves ? a->tile_waves : (four_ok ? 4 : 8);
-    p->variant = a->variant;
-    if (p->tile_waves != 4 && p->tile_waves != 8)
-      return fail(HKX_ERR_ARG, "tile_waves %d: 4 or 8", a->tile_waves);
-    if (p->tile_waves == 4 && !four_ok)
+    const bool pp_ok = bn == 256 && bm == 256;
+    int sc = a->tile_schedule;
+    if (sc == HKX_TILE_AUTO) sc = pp_ok ? HKX_TILE_PINGPONG : (four_ok ? HKX_TILE_W4 : HKX_TILE_W8);
+    if (sc != HKX_TILE_PINGPONG && sc != HKX_TILE_W4 && sc != HKX_TILE_W8)
+      return fail(HKX_ERR_ARG, "tile_schedule %d", a->tile_schedule);
+    if (sc == HKX_TILE_W4 && !four_ok)
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
+    if (sc == HKX_TILE_PINGPONG && !pp_ok)
+      return fail(HKX_ERR_ARG, "the ping-pong tile kernel takes 256x256 tiles");
+    if (a->variant & ~(HKX_PP_MFMA32 | HKX_PP_ONE_TILE) || (a->variant && sc != HKX_TILE_PINGPONG))
+      return fail(HKX_ERR_ARG, "variant %d", a->variant);
+    p->schedule = sc;
+    p->variant = a->variant;
     p->kunits = a->k * eb / 128;
   } else if (kernel == HKX_KERNEL_DECODE) {
     if (a->ab_dtype != HKX_BF16) return fail(HKX_ERR_DTYPE, "the decode kernel takes bf16");
@@ -272,13 +280,31 @@ int launched(hipError_t e, const char* what) {
   return HKX_OK;
 }
 
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mode, dim3 grid,
                          hipStream_t s) {
   const int bm = p.tile_m, bn = p.tile_n;
-  if (p.tile_waves == 4) {
-    if (bm == 256) return hkx::launch_tile4<256, 256>(t, fp8, mode, p.variant, grid, s);
-    if (bm == 128) return hkx::launch_tile4<128, 256>(t, fp8, mode, p.variant, grid, s);
-    return hkx::launch_tile4<64, 256>(t, fp8, mode, p.variant, grid, s);
+  if (p.schedule == HKX_TILE_PINGPONG) {
+    dim3 g = grid;
+    if (!(p.variant & HKX_PP_ONE_TILE)) g.x = std::min<unsigned>(g.x, (unsigned)cu_count());
+    return hkx::launch_pp(t, fp8, mode, !(p.variant & HKX_PP_MFMA32), g, s);
+  }
+  if (p.schedule == HKX_TILE_W4) {
+    if (bm == 256) return hkx::launch_tile4<256, 256>(t, fp8, mode, grid, s);
+    if (bm == 128) return hkx::launch_tile4<128, 256>(t, fp8, mode, grid, s);
+    return hkx::launch_tile4<64, 256>(t, fp8, mode, grid, s);
   }
   if (bm == 256 && bn == 256) return hkx::launch_tile<256, 256, 2>(t, fp8, mode, grid, s);
   if (bm == 128 && bn == 256) return hkx::launch_tile<128, 256, 2>(t, fp8, mode, grid, s);

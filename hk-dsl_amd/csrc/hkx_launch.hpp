@@ -16,18 +16,20 @@ template <int BM, int BN, int WM>
 hipError_t launch_tile(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
 
 template <int BM, int BN>
-hipError_t launch_tile4(const TileArgs& a, bool fp8, int mode, int variant, dim3 grid,
+hipError_t launch_tile4(const TileArgs& a, bool fp8, int mode, dim3 grid,
                         hipStream_t s);
 
 // A 16- or 8-bit C with the fused form's activation fixed at compile time (the epilogue is
 // then straight-line code); any other store takes it at run time.
 #define HKX_TILE4_STAGED(BM, BN, FP8, MODE)                                                 \
   switch (a.ep.form == HKX_EP_FUSED ? a.ep.act : HKX_ACT_NONE) {                            \
-    case HKX_ACT_GELU_TANH: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, 3, HKX_ACT_GELU_TANH>), grid, block, 0, s, a); break; \
-    case HKX_ACT_SILU: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, 3, HKX_ACT_SILU>), grid, block, 0, s, a); break;           \
-    case HKX_ACT_RELU: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, 3, HKX_ACT_RELU>), grid, block, 0, s, a); break;           \
-    default: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, 3, HKX_ACT_NONE>), grid, block, 0, s, a); break;                    \
+    case HKX_ACT_GELU_TANH: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, HKX_ACT_GELU_TANH>), grid, block, 0, s, a); break; \
+    case HKX_ACT_SILU: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, HKX_ACT_SILU>), grid, block, 0, s, a); break;           \
+    case HKX_ACT_RELU: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, HKX_ACT_RELU>), grid, block, 0, s, a); break;           \
+    default: hipLaunchKernelGGL((tile4_kernel<BM, BN, FP8, MODE, HKX_ACT_NONE>), grid, block, 0, s, a); break;                    \
   }
+
+hipError_t launch_pp(const TileArgs& a, bool fp8, int mode, bool mf16, dim3 grid, hipStream_t s);
 
 hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
                          hipStream_t s);
@@ -62,15 +64,9 @@ hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool progra
 
 #define HKX_TILE4_LAUNCHER(BM, BN)                                                           \
   template <>                                                                                \
-  hipError_t launch_tile4<BM, BN>(const TileArgs& a, bool fp8, int mode, int variant,        \
-                                  dim3 grid, hipStream_t s) {                                \
+  hipError_t launch_tile4<BM, BN>(const TileArgs& a, bool fp8, int mode, dim3 grid,        \
+                                  hipStream_t s) {                                           \
     const dim3 block(256);                                                                   \
-    if (variant == 1) { /* the direct-fill schedule of one burst a stage, for comparison */ \
-      if (mode != kStore16) return hipErrorInvalidValue;                                     \
-      if (fp8) hipLaunchKernelGGL((tile4_kernel<BM, BN, true, kStore16, 1, HKX_ACT_NONE>), grid, block, 0, s, a); \
-      else hipLaunchKernelGGL((tile4_kernel<BM, BN, false, kStore16, 1, HKX_ACT_NONE>), grid, block, 0, s, a);    \
-      return hipGetLastError();                                                              \
-    }                                                                                        \
     if (fp8) {                                                                               \
       switch (mode) {                                                                        \
         case kStore16: HKX_TILE4_STAGED(BM, BN, true, kStore16) break;                                \

@@ -27,7 +27,7 @@ namespace hkx {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, bool FP8, int MODE, int SCHED = 3, int ACT = -1>
+template <int BM, int BN, bool FP8, int MODE, int ACT = -1>
 __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   constexpr int TM = BM / 2, TN = BN / 2;
   constexpr int FM = TM / 32, FN = TN / 32;
@@ -96,16 +96,7 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
       voff[i] = (uint32_t)brow * p.ldb_b + lch16;
     }
   }
-  auto fill = [&](int kt, int s) {
-    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(kt0 + kt) * 128u);
-    uint8_t* base = smem + s * STAGE + wave * 1024;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i)
-      buf_load16_lds(i < NA ? ra : rb, base + i * 4096, voff[i], so);
-  };
-
-  // Fills [lo, hi) of a stage only: the default schedule spreads a stage's fills over
-  // three k-steps.
+  // Fills chunks [lo, hi) of a stage: a stage's fills are spread over three k-steps.
   auto fill_part = [&](int kt, int s, int lo, int hi) {
     const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(kt0 + kt) * 128u);
     uint8_t* base = smem + s * STAGE + wave * 1024;
@@ -193,8 +184,8 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   }
 
   // ---- prologue: stages 0 and 1 in flight, stage 0 landed, its first fragments read
-  fill(0, 0);
-  if (nkt > 1) fill(1, 1);
+  fill_part(0, 0, 0, NCH);
+  if (nkt > 1) fill_part(1, 1, 0, NCH);
   __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): stages 0 and 1 landed
   __syncthreads();
   read_frags(0, 0, a0, b0);
@@ -202,15 +193,12 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   // One iteration is one 128-byte K stage: KS k-steps of FM x FN MFMAs, fragment reads one
   // k-step ahead. The body is one basic block (fills and reads past the last stage are
   // kept, pointed at the last stage again, and never used), so the MFMAs, the reads and
-  // the fills are interleaved by sched_group_barrier:
-  //
-  // * SCHED 3 (the default): the next tile's fills -- into the stage freed at this
-  //   iteration's barrier -- start under the last k-step (3/8 of them) and go on under
-  //   the next iteration's first two k-steps. A burst of fills blocks the wave's
-  //   in-order issue (every wave of the CU issues its 16 at once and they queue at the
-  //   address unit), so spread out they cost a third less; spread over three k-steps
-  //   they still land before the barrier that waits for them.
-  // * SCHED 1: all the fills in one burst under the last k-step (for comparison).
+  // the fills are interleaved by sched_group_barrier: the next tile's fills -- into the
+  // stage freed at this iteration's barrier -- start under the last k-step (3/8 of them)
+  // and go on under the next iteration's first two k-steps. A burst of fills blocks the
+  // wave's in-order issue (every wave of the CU issues its 16 at once and they queue at
+  // the address unit), so spread out they cost a third less; spread over three k-steps
+  // they still land before the barrier that waits for them.
   constexpr int NRD = FP8 ? 2 * (FM + FN) : (FM + FN);  // ds_read_b128 per k-step
   for (int kt = 0; kt < nkt; ++kt) {
     const int s = kt & 1;
@@ -224,7 +212,7 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
         read_frags(s, ks + 1, a1, b1);
         mma(a0, b0);
       }
-      if constexpr (SCHED == 3) {
+      {
         // the rest of tile kt + 1's fills, begun under iteration kt - 1's last k-step
         constexpr int F0 = NCH * 3 / 8, F1 = NCH * 11 / 16;
         if (KS == 2) {
@@ -241,13 +229,6 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
         }
         __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, NCH, 0);
-      } else {
-#pragma unroll
-        for (int q = 0; q < NRD; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -257,10 +238,7 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
     // buffer loads)
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
     __syncthreads();
-    if constexpr (SCHED == 3)
-      fill_part(min(kt + 2, nkt - 1), s, 0, NCH * 3 / 8);
-    else
-      fill(min(kt + 2, nkt - 1), s);
+    fill_part(min(kt + 2, nkt - 1), s, 0, NCH * 3 / 8);
     // KS is even: step KS-1 multiplies set 1 while the next stage's step 0 reads set 0
     read_frags(s ^ 1, 0, a0, b0);
     mma(a1, b1);
@@ -268,7 +246,7 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
     for (int q = 0; q < NRD; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, SCHED == 3 ? 1 : NCH / NRD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NRD, 0);
     __builtin_amdgcn_sched_group_barrier(0x020, NCH, 0);

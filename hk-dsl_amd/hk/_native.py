@@ -27,6 +27,10 @@ ROW, COL, TILE = 1, 2, 3
 EP_NONE, EP_FUSED, EP_PROGRAM, EP_SILU_MUL = range(4)
 ACT_NONE, ACT_GELU_TANH, ACT_SILU, ACT_RELU = range(4)
 KERNEL_AUTO, KERNEL_TILE, KERNEL_DECODE = range(3)
+TILE_AUTO, TILE_PINGPONG, TILE_W4, TILE_W8 = range(4)
+PP_MFMA32, PP_ONE_TILE = 1, 2
+#: The tile schedules by name (the route candidates' "schedule").
+SCHEDULES = {"pp": TILE_PINGPONG, "w4": TILE_W4, "w8": TILE_W8}
 
 OPS = ["MOV", "LOAD", "CONST", "ROW", "COL", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN",
        "EXP", "EXP2", "LOG", "LOG2", "ABS", "RELU", "GELU", "SILU", "SQRT", "RSQRT",
@@ -58,7 +62,7 @@ class HkxGemmArgs(Structure):
                 ("ldb", c_int64), ("ldc", c_int64), ("m", c_int32), ("n", c_int32),
                 ("k", c_int32), ("ab_dtype", c_int32), ("c_dtype", c_int32),
                 ("kernel", c_int32), ("tile_m", c_int32), ("tile_n", c_int32),
-                ("splits", c_int32), ("tile_waves", c_int32), ("variant", c_int32),
+                ("splits", c_int32), ("tile_schedule", c_int32), ("variant", c_int32),
                 ("decode_waves", c_int32), ("decode_rows", c_int32),
                 ("ws", c_void_p), ("ws_bytes", c_size_t), ("ep", HkxEpilogue)]
 
@@ -163,7 +167,7 @@ def workspace(device, nbytes: int):
     return buf
 
 
-def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, tile_waves=0,
+def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, schedule=TILE_AUTO,
               variant=0, decode_waves=0, decode_rows=0, ep: HkxEpilogue = None) -> HkxGemmArgs:
     """HkxGemmArgs for A (M, K), B (N, K) -- (2N, K) paired -- and C (M, N) tensors."""
     args = HkxGemmArgs()
@@ -174,7 +178,7 @@ def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, tile
     args.ab_dtype = dtype_code(a.dtype)
     args.c_dtype = dtype_code(c.dtype)
     args.kernel, args.tile_m, args.tile_n, args.splits = kernel, tile_m, tile_n, splits
-    args.tile_waves, args.variant = tile_waves, variant
+    args.tile_schedule, args.variant = schedule, variant
     args.decode_waves, args.decode_rows = decode_waves, decode_rows
     if ep is not None:
         args.ep = ep

@@ -72,7 +72,8 @@ def scaled_mm(a, b, scale_a, scale_b, *, bias=None, out=None, schedule=None):
         ep.ops[2] = nat.HkxOperand(bb.data_ptr(), nat.ROW, nat.BF16, 1)
         ep.row_add, ep.nops = 2, 3
     args = nat.gemm_args(a, b, out, kernel=nat.KERNEL_TILE, tile_m=rec["tile_m"],
-                         tile_n=rec["tile_n"], tile_waves=rec.get("waves", 4),
+                         tile_n=rec["tile_n"], schedule=nat.SCHEDULES[rec["schedule"]],
+                         variant=rec.get("variant", 0),
                          splits=rec.get("splits", 1), ep=ep)
     nat.run(args, a.device)
     del keep

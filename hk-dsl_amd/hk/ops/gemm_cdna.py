@@ -5,8 +5,9 @@ measured table (the nearest M on a log scale for that N x K), else a rule (decod
 M <= 32, small blocks to M 2048, the 256 x 256 pingpong above). This is the same
 contract over this build's kernels:
 
-* `CANDIDATES` -- the schedules a route may name: the 4-wave 32x32-MFMA tile kernel at
-  256 / 128 / 64 rows, the 8-wave 16x16-MFMA one, their split-K forms, the decode kernel;
+* `CANDIDATES` -- the schedules a route may name: the ping-pong kernel at 256 x 256, the
+  4-wave 32x32-MFMA tile kernel at 256 / 128 / 64 rows, the 8-wave 16x16-MFMA one, their
+  split-K forms, the decode kernel;
 * `route(m, n, k)` -- a user record (`OVERRIDE`), else the measured table
   `hk/tuned/routes_gemm_gfx950.json` (this build's own measurements), else `rule`;
 * `resolve` -- a candidate made concrete for a shape (the decode kernel's split);
@@ -29,20 +30,27 @@ BLOCK_N_MIN = 4
 CUS = 256
 
 CANDIDATES: Dict[str, Dict[str, Any]] = {
-    "t256": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 4},
-    "t128": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4},
-    "t64": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4},
-    "t256w8": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 8},
-    "t128w8": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 8},
-    "t64w8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 8},
-    "t128n128": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "waves": 8},
-    "t256n128": {"kernel": "tile", "tile_m": 256, "tile_n": 128, "waves": 8},
-    "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "waves": 4, "splits": 2},
-    "t128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4, "splits": 2},
-    "t128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "waves": 4, "splits": 4},
-    "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 2},
-    "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 4},
-    "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "waves": 4, "splits": 8},
+    # 256 x 256: the ping-pong kernel (8 waves, two a SIMD; 16 x 16 MFMAs, one workgroup a
+    # CU walking its tiles), and its variants for measurement
+    "t256": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp"},
+    "t256m32": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 1},
+    "t256g": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 2},
+    "t256w4": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "w4"},
+    "t256w8": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "w8"},
+    # smaller tiles: the 4-wave kernel (32 x 32 MFMAs), the 8-wave one (16 x 16)
+    "t128": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4"},
+    "t64": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4"},
+    "t128w8": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w8"},
+    "t64w8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w8"},
+    "t128n128": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "schedule": "w8"},
+    "t256n128": {"kernel": "tile", "tile_m": 256, "tile_n": 128, "schedule": "w8"},
+    # split over K
+    "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "splits": 2},
+    "t128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 2},
+    "t128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 4},
+    "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},
+    "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 4},
+    "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 8},
     "decode": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto"},
     "decode_w4": {"kernel": "decode", "waves": 4, "rows": 16, "splits": "auto"},
     "decode_w16": {"kernel": "decode", "waves": 16, "rows": 16, "splits": "auto"},

@@ -433,7 +433,8 @@ class KernelDesc:
     sched: Dict[str, Any]
 
     def source(self) -> str:
-        return {"tile": "hk-dsl_amd/csrc/hkx_tile4.hpp (4 waves) / hkx_tile.hpp (8 waves)",
+        return {"tile": "hk-dsl_amd/csrc/hkx_pp.hpp (ping-pong) / hkx_tile4.hpp (4 waves) / "
+                        "hkx_tile.hpp (8 waves)",
                 "decode": "hk-dsl_amd/csrc/hkx_decode.hpp",
                 "reduce": "hk-dsl_amd/csrc/hkx_reduce.hpp"}[self.name.split("<")[0]]
 
@@ -442,7 +443,7 @@ def kernel_for(step: Step, ep: Optional[Epilogue] = None, arch: Optional[str] = 
     """The kernel a step launches (with the epilogue if the step carries it)."""
     s = step.sched
     if step.kernel == "tile":
-        name = (f"tile<{s['tile_m']}x{s['tile_n']}, waves {s.get('waves', 4)}, "
+        name = (f"tile<{s['tile_m']}x{s['tile_n']}, {s['schedule']}, "
                 f"splits {s.get('splits', 1)}>")
     elif step.kernel == "decode":
         name = (f"decode<waves {s.get('waves', 8)}, rows {s.get('rows', 16)}, "
@@ -508,7 +509,7 @@ class _Launch:
         if st.kernel == "tile":
             args.kernel = nat.KERNEL_TILE
             args.tile_m, args.tile_n = s["tile_m"], s["tile_n"]
-            args.tile_waves = s.get("waves", 4)
+            args.tile_schedule = nat.SCHEDULES[s["schedule"]]
             args.variant = s.get("variant", 0)
         else:
             args.kernel = nat.KERNEL_DECODE

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define HKX_ABI_VERSION 1
+#define HKX_ABI_VERSION 2
 
 /* Status codes. */
 #define HKX_OK 0
@@ -143,6 +143,16 @@ typedef struct HkxEpilogue {
 #define HKX_KERNEL_TILE 1   /* LDS-tiled MFMA GEMM, tile_m x tile_n blocks, optional split-K */
 #define HKX_KERNEL_DECODE 2 /* skinny-M weight-streaming GEMM (M <= 32), optional split-K */
 
+/* Tile kernel schedules (HkxGemmArgs.tile_schedule). */
+#define HKX_TILE_AUTO 0
+#define HKX_TILE_PINGPONG 1 /* 8 waves, two a SIMD taking turns at the MFMA; 256 x 256 only */
+#define HKX_TILE_W4 2       /* 4 waves, one a SIMD (2 x 2, 32 x 32 MFMAs); tile_n 256 */
+#define HKX_TILE_W8 3       /* 8 waves, register-staged fills, 16 x 16 MFMAs; any tile shape */
+
+/* HKX_TILE_PINGPONG variant bits (HkxGemmArgs.variant; 0 = the default). */
+#define HKX_PP_MFMA32 1   /* 32 x 32 MFMA fragments (the fp8 and paired forms always use them) */
+#define HKX_PP_ONE_TILE 2 /* one tile a workgroup, instead of a grid of one workgroup a CU */
+
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */
   const void* b; /* (N, K) -- (2N, K) for HKX_EP_SILU_MUL -- row stride ldb elements */
@@ -155,9 +165,9 @@ typedef struct HkxGemmArgs {
   int32_t tile_m;   /* TILE: 64, 128 or 256 */
   int32_t tile_n;   /* TILE: 128 or 256 */
   int32_t splits;   /* >= 1; > 1 stores fp32 shares to ws and sums them in order */
-  int32_t tile_waves; /* TILE: 4 (2 x 2 waves, 32 x 32 MFMAs; tile_n 256 only) or 8; 0 = 4
-                         where the tile takes it */
-  int32_t variant;  /* TILE: schedule variant of the K loop, 0 = the default (for tuning) */
+  int32_t tile_schedule; /* TILE: HKX_TILE_*; AUTO = PINGPONG for 256 x 256 tiles, else W4
+                            where the tile takes it, else W8 */
+  int32_t variant;  /* TILE, PINGPONG: HKX_PP_* bits (for tuning); 0 elsewhere */
   int32_t decode_waves; /* DECODE: waves per workgroup (4, 8 or 16); 0 = default */
   int32_t decode_rows;  /* DECODE: W rows per workgroup (16 or 32); 0 = default */
   void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */

@@ -27,7 +27,7 @@ def test_the_library_exports_every_declared_symbol():
     assert set(names) == set(nat.SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.hkx_abi_version() == 1
+    assert L.hkx_abi_version() == 2
 
 
 def test_no_kernel_launch_stub_is_missing():

@@ -41,10 +41,20 @@ def _run(a, b, c, **kw):
     torch.cuda.synchronize()
 
 
-#: (tile_m, tile_n, waves): the 4-wave (32 x 32 MFMA) and 8-wave (16 x 16 MFMA) kernels
-TILES = [(256, 256, 4), (128, 256, 4), (64, 256, 4), (256, 256, 8), (128, 256, 8),
-         (64, 256, 8), (128, 128, 8), (256, 128, 8)]
-TILE_IDS = [f"{m}x{n}w{w}" for m, n, w in TILES]
+PP, W4, W8 = nat.TILE_PINGPONG, nat.TILE_W4, nat.TILE_W8
+SNAME = {PP: "pp", W4: "w4", W8: "w8"}
+#: (tile_m, tile_n, schedule, variant): the ping-pong kernel (16 x 16 and 32 x 32 MFMAs, one
+#: workgroup a CU or one a tile), the 4-wave (32 x 32 MFMA) and 8-wave (16 x 16) kernels
+TILES = [(256, 256, PP, 0), (256, 256, PP, nat.PP_MFMA32), (256, 256, PP, nat.PP_ONE_TILE),
+         (256, 256, W4, 0), (128, 256, W4, 0), (64, 256, W4, 0), (256, 256, W8, 0),
+         (128, 256, W8, 0), (64, 256, W8, 0), (128, 128, W8, 0), (256, 128, W8, 0)]
+
+
+def tile_id(t):
+    return f"{t[0]}x{t[1]}{SNAME[t[2]]}" + (f"v{t[3]}" if len(t) > 3 and t[3] else "")
+
+
+TILE_IDS = [tile_id(t) for t in TILES]
 
 
 @pytest.mark.parametrize("tile", TILES, ids=TILE_IDS)
@@ -56,13 +66,13 @@ def test_tile_plain_bf16(tile, shape):
     ref = O.gemm_fp32(a, b)
     c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
     _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1],
-         tile_waves=tile[2])
+         schedule=tile[2], variant=tile[3])
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP)], ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
-def test_tile_bias_gelu_and_split(splits, waves):
+def test_tile_bias_gelu_and_split(splits, tile):
     m, n, k = 200, 1408, 640
     a, b = _data(m, n, k, seed=1)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
@@ -70,8 +80,8 @@ def test_tile_bias_gelu_and_split(splits, waves):
     c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     bd = bias.to(DEV)
     ep = _fused([(bd, nat.ROW)], act=nat.ACT_GELU_TANH, ra=0)
-    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256, splits=splits,
-         tile_waves=waves, ep=ep)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=256,
+         splits=splits, schedule=tile[1], ep=ep)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
@@ -84,9 +94,10 @@ def test_tile_nothing_past_m():
     assert torch.equal(room[m:].cpu(), torch.full((8, n), 7.0, dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("sched", [(W4, 0), (W8, 0), (PP, 0), (PP, nat.PP_MFMA32)],
+                         ids=lambda t: SNAME[t[0]] + str(t[1]))
 @pytest.mark.parametrize("out", [torch.float32, torch.float16])
-def test_tile_out_dtypes_residual_colscale(out, waves):
+def test_tile_out_dtypes_residual_colscale(out, sched):
     m, n, k = 300, 768, 512
     a, b = _data(m, n, k, seed=3)
     g = torch.Generator().manual_seed(9)
@@ -97,12 +108,12 @@ def test_tile_out_dtypes_residual_colscale(out, waves):
     resd, rsd = res.to(DEV), rs.to(DEV)
     ep = _fused([(rsd, nat.COL), (resd, nat.TILE)], cs=0, ta=1)
     _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, ep=ep,
-         tile_waves=waves)
+         schedule=sched[0], variant=sched[1])
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile", [(256, 256, 4), (64, 256, 4), (256, 256, 8), (128, 128, 8)],
-                         ids=lambda t: f"{t[0]}x{t[1]}w{t[2]}")
+@pytest.mark.parametrize("tile", [(256, 256, PP), (256, 256, W4), (64, 256, W4), (256, 256, W8),
+                                  (128, 128, W8)], ids=tile_id)
 def test_tile_fp8_scaled(tile):
     m, n, k = 300, 512, 1024
     g = torch.Generator().manual_seed(11)
@@ -116,13 +127,13 @@ def test_tile_fp8_scaled(tile):
     sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
     ep = _fused([(sad, nat.COL), (sbd, nat.ROW)], cs=0, rs=1)
     _run(a8.to(DEV), b8.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1],
-         tile_waves=tile[2], ep=ep)
+         schedule=tile[2], ep=ep)
     assert O.rel_to_max(c.cpu(), ref) < 1e-4
     # with the bias, into bf16
     c2 = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     ep = _fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)], cs=0, rs=1, ra=2)
     _run(a8.to(DEV), b8.to(DEV), c2, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1],
-         tile_waves=tile[2], ep=ep)
+         schedule=tile[2], ep=ep)
     O.assert_close(c2, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
 
 
@@ -142,14 +153,15 @@ def test_decode(m, cfg):
 
 
 @pytest.mark.parametrize("kernel", ["tile", "tile_split", "decode", "decode_split", "tile_fp32",
-                                    "tile8", "tile8_split"])
+                                    "tile8", "tile8_split", "tilepp", "tilepp_split",
+                                    "tilepp_fp32"])
 def test_silu_and_mul(kernel):
     m = 5 if kernel.startswith("decode") else 300
     n, k = 768, 512
     a, b = _data(m, 2 * n, k, seed=7)
     acc = O.gemm_fp32(a, b)
     ref = O.silu_and_mul(acc[:, :n], acc[:, n:])
-    dt = torch.float32 if kernel == "tile_fp32" else torch.bfloat16
+    dt = torch.float32 if kernel.endswith("fp32") else torch.bfloat16
     c = torch.empty((m, n), dtype=dt, device=DEV)
     ep = nat.HkxEpilogue()
     ep.form = nat.EP_SILU_MUL
@@ -158,7 +170,8 @@ def test_silu_and_mul(kernel):
         kw.update(kernel=nat.KERNEL_DECODE, decode_rows=32)
     else:
         kw.update(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
-                  tile_waves=8 if kernel.startswith("tile8") else 4)
+                  schedule=W8 if kernel.startswith("tile8") else (PP if kernel.startswith("tilepp")
+                                                                  else W4))
     _run(a.to(DEV), b.to(DEV), c, **kw)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
@@ -190,29 +203,30 @@ def test_program_pass():
         ep.ins[i] = nat.HkxInstr(P[op], d, x, y, z, 0, 0, 0, imm)
     ep.nins, ep.out_reg = len(prog), 1
     for kw in (dict(kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256),
+               dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=PP),
                dict(kernel=nat.KERNEL_TILE, tile_m=64, tile_n=256, splits=2),
-               dict(kernel=nat.KERNEL_TILE, tile_m=128, tile_n=128, tile_waves=8)):
+               dict(kernel=nat.KERNEL_TILE, tile_m=128, tile_n=128, schedule=nat.TILE_W8)):
         c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
         _run(a.to(DEV), b.to(DEV), c, ep=ep, **kw)
         O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("waves", [4, 8])
-def test_quantizing_stores(waves):
+@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP)], ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
+def test_quantizing_stores(tile):
     m, n, k = 128, 512, 512
     a, b = _data(m, n, k, seed=12)
     acc = O.gemm_fp32(a, b)
     s = torch.full((n,), 40.0)
     sd = s.to(DEV)
     c = torch.empty((m, n), dtype=torch.int8, device=DEV)
-    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256,
-         tile_waves=waves, ep=_fused([(sd, nat.ROW)], rs=0))
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=256,
+         schedule=tile[1], ep=_fused([(sd, nat.ROW)], rs=0))
     assert (c.cpu().float() - O.quantize_int8(acc * 40)).abs().max().item() <= 1.0
     c8 = torch.empty((m, n), dtype=torch.float8_e4m3fn, device=DEV)
     s2 = torch.rand(n, generator=torch.Generator().manual_seed(3)) * 900
     s2d = s2.to(DEV)
-    _run(a.to(DEV), b.to(DEV), c8, kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256,
-         tile_waves=waves, ep=_fused([(s2d, nat.ROW)], rs=0))
+    _run(a.to(DEV), b.to(DEV), c8, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=256,
+         schedule=tile[1], ep=_fused([(s2d, nat.ROW)], rs=0))
     want = (acc * s2).clamp(-448, 448)
     got = c8.cpu().float()
     big = want.abs() > 16
