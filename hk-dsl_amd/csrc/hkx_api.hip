@@ -48,7 +48,8 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 struct Plan {
   int kernel;     // HKX_KERNEL_TILE / _DECODE
   int tile_m, tile_n, wm;
-  int schedule;   // HKX_TILE_PINGPONG: pp_kernel, _W4: tile4_kernel, _W8: tile_kernel
+  int schedule;   // HKX_TILE_RING: ring_kernel, _PINGPONG: pp_kernel, _W4: tile4_kernel,
+                  // _W8: tile_kernel
   int variant;
   int waves, fn, mf;  // decode
   int splits;     // effective (no empty split)
@@ -203,9 +204,11 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     const bool four_ok = bn == 256 && (bm == 256 || bm == 128 || bm == 64);
     const bool pp_ok = bn == 256 && bm == 256;
     int sc = a->tile_schedule;
-    if (sc == HKX_TILE_AUTO) sc = pp_ok ? HKX_TILE_PINGPONG : (four_ok ? HKX_TILE_W4 : HKX_TILE_W8);
-    if (sc != HKX_TILE_PINGPONG && sc != HKX_TILE_W4 && sc != HKX_TILE_W8)
+    if (sc == HKX_TILE_AUTO) sc = pp_ok ? HKX_TILE_RING : (four_ok ? HKX_TILE_W4 : HKX_TILE_W8);
+    if (sc != HKX_TILE_PINGPONG && sc != HKX_TILE_W4 && sc != HKX_TILE_W8 && sc != HKX_TILE_RING)
       return fail(HKX_ERR_ARG, "tile_schedule %d", a->tile_schedule);
+    if (sc == HKX_TILE_RING && !pp_ok)
+      return fail(HKX_ERR_ARG, "the ring tile kernel takes 256x256 tiles");
     if (sc == HKX_TILE_W4 && !four_ok)
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
     if (sc == HKX_TILE_PINGPONG && !pp_ok)
@@ -296,6 +299,15 @@ int cu_count() {
 hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mode, dim3 grid,
                          hipStream_t s) {
   const int bm = p.tile_m, bn = p.tile_n;
+  // The ring kernel: one workgroup a CU (a split's share of them) walking its tiles. A call
+  // it does not take (an unaligned C, N % 8 != 0, a strided 16-bit column scale) runs on
+  // the ping-pong kernel, which takes every 256 x 256 call.
+  if (p.schedule == HKX_TILE_RING && hkx::ring_takes(t, fp8, mode)) {
+    dim3 g = grid;
+    g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
+    return hkx::launch_ring(t, fp8, mode, g, s);
+  }
+  if (p.schedule == HKX_TILE_RING) return hkx::launch_pp(t, fp8, mode, true, grid, s);
   if (p.schedule == HKX_TILE_PINGPONG) {
     dim3 g = grid;
     if (!(p.variant & HKX_PP_ONE_TILE)) g.x = std::min<unsigned>(g.x, (unsigned)cu_count());

@@ -31,6 +31,13 @@ hipError_t launch_tile4(const TileArgs& a, bool fp8, int mode, dim3 grid,
 
 hipError_t launch_pp(const TileArgs& a, bool fp8, int mode, bool mf16, dim3 grid, hipStream_t s);
 
+// The persistent ring kernel (hkx_ring.hpp): grid.x workgroups, each every grid.x-th tile.
+// Returns hipErrorInvalidValue for a call it does not take (ring_takes is false).
+bool ring_takes(const TileArgs& a, bool fp8, int mode);
+hipError_t launch_ring(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
+hipError_t launch_ring_bf16(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
+hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
+
 hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
                          hipStream_t s);
 

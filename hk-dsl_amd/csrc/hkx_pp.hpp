@@ -35,7 +35,6 @@
 
 namespace hkx {
 
-HKX_DEV int swz4(int r) { return ((r >> 4) & 1) | ((r >> 2) & 2); }
 
 template <bool FP8, int MODE, int ACT = -1, bool MF16 = false>
 __global__ void __launch_bounds__(512, 1) pp_kernel(const TileArgs p) {

@@ -1,0 +1,26 @@
+// The persistent ring GEMM kernel, fp8 e4m3 instantiations.
+#include "hkx_launch.hpp"
+#include "hkx_ring.hpp"
+
+namespace hkx {
+
+#define HKX_RING(MODE, ACT, EPF) hipLaunchKernelGGL((ring_kernel<true, MODE, ACT, EPF>), grid, block, 0, s, a)
+
+hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s) {
+  const dim3 block(512);
+  switch (mode) {
+    case kStore16:
+      if (epf == kEpNone && act == HKX_ACT_NONE) HKX_RING(kStore16, HKX_ACT_NONE, kEpNone);
+      else if (epf == kEpBias && act == HKX_ACT_NONE) HKX_RING(kStore16, HKX_ACT_NONE, kEpBias);
+      else if (epf == kEpDeq) HKX_RING(kStore16, HKX_ACT_NONE, kEpDeq);
+      else if (epf == kEpDeqBias) HKX_RING(kStore16, HKX_ACT_NONE, kEpDeqBias);
+      else HKX_RING(kStore16, -1, kEpGeneric);
+      break;
+    case kStore8: HKX_RING(kStore8, -1, kEpGeneric); break;
+    case kStoreF32: HKX_RING(kStoreF32, -1, kEpGeneric); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hkx

@@ -59,6 +59,11 @@ constexpr int kPairWs = 4;    // gate and up fp32 shares, (M, 2N) per split
 
 HKX_DEV int swz(int j) { return (j ^ (j >> 3)) & 7; }
 
+// The swizzle of rows of four 16-byte chunks (64-byte half-stage rows): chunk c of row r is
+// stored at c ^ swz4(r), bits 4 and 3 of the row, which makes the fragment reads of 32
+// rows with one chunk each conflict-free.
+HKX_DEV int swz4(int r) { return ((r >> 4) & 1) | ((r >> 2) & 2); }
+
 template <int BM, int BN, int WM, bool FP8, int MODE>
 __global__ void __launch_bounds__(512, 1) tile_kernel(const TileArgs p) {
   constexpr int WN = 8 / WM;

@@ -27,10 +27,10 @@ ROW, COL, TILE = 1, 2, 3
 EP_NONE, EP_FUSED, EP_PROGRAM, EP_SILU_MUL = range(4)
 ACT_NONE, ACT_GELU_TANH, ACT_SILU, ACT_RELU = range(4)
 KERNEL_AUTO, KERNEL_TILE, KERNEL_DECODE = range(3)
-TILE_AUTO, TILE_PINGPONG, TILE_W4, TILE_W8 = range(4)
+TILE_AUTO, TILE_PINGPONG, TILE_W4, TILE_W8, TILE_RING = range(5)
 PP_MFMA32, PP_ONE_TILE = 1, 2
 #: The tile schedules by name (the route candidates' "schedule").
-SCHEDULES = {"pp": TILE_PINGPONG, "w4": TILE_W4, "w8": TILE_W8}
+SCHEDULES = {"pp": TILE_PINGPONG, "w4": TILE_W4, "w8": TILE_W8, "ring": TILE_RING}
 
 OPS = ["MOV", "LOAD", "CONST", "ROW", "COL", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN",
        "EXP", "EXP2", "LOG", "LOG2", "ABS", "RELU", "GELU", "SILU", "SQRT", "RSQRT",

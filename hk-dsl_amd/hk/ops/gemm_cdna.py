@@ -5,7 +5,7 @@ measured table (the nearest M on a log scale for that N x K), else a rule (decod
 M <= 32, small blocks to M 2048, the 256 x 256 pingpong above). This is the same
 contract over this build's kernels:
 
-* `CANDIDATES` -- the schedules a route may name: the ping-pong kernel at 256 x 256, the
+* `CANDIDATES` -- the schedules a route may name: the ring and ping-pong kernels at 256 x 256, the
   4-wave 32x32-MFMA tile kernel at 256 / 128 / 64 rows, the 8-wave 16x16-MFMA one, their
   split-K forms, the decode kernel;
 * `route(m, n, k)` -- a user record (`OVERRIDE`), else the measured table
@@ -30,11 +30,14 @@ BLOCK_N_MIN = 4
 CUS = 256
 
 CANDIDATES: Dict[str, Dict[str, Any]] = {
-    # 256 x 256: the ping-pong kernel (8 waves, two a SIMD; 16 x 16 MFMAs, one workgroup a
-    # CU walking its tiles), and its variants for measurement
-    "t256": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp"},
-    "t256m32": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 1},
-    "t256g": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 2},
+    # 256 x 256: the ring kernel (8 waves taking turns at the MFMA, one workgroup a CU
+    # walking its tiles through one LDS ring, the epilogue stored from registers), and the
+    # ping-pong kernel it is measured against (one tile a workgroup; "t256ppc": one
+    # workgroup a CU; "t256m32": 32 x 32 MFMA fragments)
+    "t256": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring"},
+    "t256pp": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 2},
+    "t256ppc": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp"},
+    "t256m32": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "variant": 3},
     "t256w4": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "w4"},
     "t256w8": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "w8"},
     # smaller tiles: the 4-wave kernel (32 x 32 MFMAs), the 8-wave one (16 x 16)
@@ -45,7 +48,7 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     "t128n128": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "schedule": "w8"},
     "t256n128": {"kernel": "tile", "tile_m": 256, "tile_n": 128, "schedule": "w8"},
     # split over K
-    "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "pp", "splits": 2},
+    "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "splits": 2},
     "t128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 2},
     "t128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 4},
     "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},

@@ -148,6 +148,9 @@ typedef struct HkxEpilogue {
 #define HKX_TILE_PINGPONG 1 /* 8 waves, two a SIMD taking turns at the MFMA; 256 x 256 only */
 #define HKX_TILE_W4 2       /* 4 waves, one a SIMD (2 x 2, 32 x 32 MFMAs); tile_n 256 */
 #define HKX_TILE_W8 3       /* 8 waves, register-staged fills, 16 x 16 MFMAs; any tile shape */
+#define HKX_TILE_RING 4     /* 8 waves taking turns at the MFMA, one workgroup a CU walking its
+                               tiles through one LDS ring, epilogue stored from registers;
+                               256 x 256 only, C rows 16-byte aligned, N % 8 == 0 */
 
 /* HKX_TILE_PINGPONG variant bits (HkxGemmArgs.variant; 0 = the default). */
 #define HKX_PP_MFMA32 1   /* 32 x 32 MFMA fragments (the fp8 and paired forms always use them) */
@@ -165,8 +168,9 @@ typedef struct HkxGemmArgs {
   int32_t tile_m;   /* TILE: 64, 128 or 256 */
   int32_t tile_n;   /* TILE: 128 or 256 */
   int32_t splits;   /* >= 1; > 1 stores fp32 shares to ws and sums them in order */
-  int32_t tile_schedule; /* TILE: HKX_TILE_*; AUTO = PINGPONG for 256 x 256 tiles, else W4
-                            where the tile takes it, else W8 */
+  int32_t tile_schedule; /* TILE: HKX_TILE_*; AUTO = RING for 256 x 256 tiles it takes,
+                            else PINGPONG for 256 x 256, else W4 where the tile takes it,
+                            else W8 */
   int32_t variant;  /* TILE, PINGPONG: HKX_PP_* bits (for tuning); 0 elsewhere */
   int32_t decode_waves; /* DECODE: waves per workgroup (4, 8 or 16); 0 = default */
   int32_t decode_rows;  /* DECODE: W rows per workgroup (16 or 32); 0 = default */
