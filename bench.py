@@ -123,6 +123,10 @@ def main():
     value = flops * args.steps / wall / 1e12
     achieved = flops / mean_s / 1e12
     plan = T.plan(m, n, k)
+    sched = plan[0].sched.get("schedule")
+    kname = {"ring": "hkx::ring_kernel<bf16, kStore16, GELU_TANH, kEpBias>",
+             "pp": "hkx::pp_kernel<bf16, kStore16, GELU_TANH, mfma16>",
+             "w4": "hkx::tile4_kernel<256, 256, bf16, kStore16, GELU_TANH>"}.get(sched, str(sched))
     res = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
@@ -133,7 +137,7 @@ def main():
                    "route": plan[0].route, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
-                     "kernel": "hkx::tile4_kernel<256,256,bf16,kStore16>",
+                     "kernel": kname,
                      "avg_launch_us": round(mean_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
                      "algorithmic_flops_per_launch": flops},
     }

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -231,6 +232,8 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     p->fn = rows / 16;
     p->mf = a->m <= 16 ? 1 : 2;
     p->kunits = a->k / 128;
+    if (a->variant & ~HKX_DEC_STREAM) return fail(HKX_ERR_ARG, "decode variant %d", a->variant);
+    p->variant = a->variant;
   } else {
     return fail(HKX_ERR_ARG, "kernel %d", kernel);
   }
@@ -282,6 +285,11 @@ int launched(hipError_t e, const char* what) {
     return fail(HKX_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
   return HKX_OK;
 }
+
+// Tile rows of the grouped raster: consecutive tiles go down a group of this many tile
+// rows, then on to the next column. With the XCD-chunked numbering each XCD's share of a
+// 4096 x 12288 call is then 8 x 12 tiles (A and B panels: 40 MB) rather than 4 x 24 (56 MB).
+constexpr int kWgmRows = 8;
 
 int cu_count() {
   static int cached[64] = {0};
@@ -387,7 +395,7 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
     const int outw = p.pair ? p.tile_n / 2 : p.tile_n;
     t.tiles_m = (a.m + p.tile_m - 1) / p.tile_m;
     t.tiles_n = (a.n + outw - 1) / outw;
-    t.wgm = 4;
+    t.wgm = kWgmRows;
     t.pair_off = a.n;
     t.c_dt = a.c_dtype;
     const dim3 grid(t.tiles_m * t.tiles_n, p.splits);
@@ -443,7 +451,12 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       d.ep = fused;
       mode = p.pair ? hkx::kDecPair : hkx::kDecOut;
     }
-    rc = launched(hkx::launch_decode(d, p.waves, p.fn, p.mf, mode, grid, s), "decode GEMM");
+    if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair)) {
+      const dim3 g(std::min((a.n + 15) / 16, cu_count()));
+      rc = launched(hkx::launch_stream(d, g, s), "decode GEMM");
+    } else {
+      rc = launched(hkx::launch_decode(d, p.waves, p.fn, p.mf, mode, grid, s), "decode GEMM");
+    }
     if (rc) return rc;
   }
 

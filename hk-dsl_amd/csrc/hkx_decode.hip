@@ -43,4 +43,21 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
   return launch_fn<16>(a, fn, mf, mode, grid, s);
 }
 
+bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
+  const int groups = a.g_total;  // 128-element K groups
+  return splits == 1 && !pair && a.M <= 16 && groups % 8 == 0 && groups <= 32;
+}
+
+hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(512);
+  switch (a.g_total / 8) {
+    case 1: hipLaunchKernelGGL((stream_kernel<1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((stream_kernel<2>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((stream_kernel<3>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((stream_kernel<4>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace hkx

@@ -36,6 +36,9 @@ struct DecodeArgs {
   Fused ep;
 };
 
+// s_waitcnt vmcnt(n) (gfx9 encoding: bits 3:0 and 15:14; expcnt and lgkmcnt left alone)
+constexpr int wait_vm_dec(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 constexpr int kDecOut = 0;     // C with the fused epilogue
 constexpr int kDecWs = 1;      // fp32 shares, (M, N) per split
 constexpr int kDecPair = 2;    // silu(gate) * up into C
@@ -157,6 +160,130 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
       }
     }
   }
+}
+
+
+// The streaming decode GEMM: one workgroup a CU walks the 16-row blocks of W (every
+// gridDim.x-th), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
+// 1024 up to 1024 CPB.
+//
+// * W goes HBM -> LDS by buffer loads (`buffer_load_dwordx4 ... lds`), each instruction 1 KB
+//   of one row, contiguous -- the access a pure streaming read reaches HBM's ceiling with --
+//   in chunks of 16 rows x 1024 K (32 KB) through a ring of four: chunk q + 3 is in flight
+//   while chunk q is multiplied. A row's 128 16-byte pieces are stored XOR-swizzled by the
+//   row (piece c at c ^ (r % 16)), applied on the global side, so the MFMA fragment reads
+//   (16 rows, one piece each) are conflict-free.
+// * X is the same for every block: wave w owns the 128-element group w of every chunk, and
+//   loads its share of X (CPB groups of 16 rows) into registers once.
+// * v_mfma_f32_16x16x32_bf16 with W's fragment first; the 8 waves' partial sums of a block
+//   meet in LDS (double-buffered by block parity), and wave 0 sums, applies the epilogue and
+//   stores after the next chunk's barrier, under the other waves' MFMAs.
+template <int CPB>
+__global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
+  constexpr int NW = 8;
+  constexpr int CH = 16 * 2048;  // a chunk: 16 rows x 2 KB
+  constexpr int NR = 4;          // ring slots
+  constexpr int RED = NR * CH;   // then the partial sums: [block parity][wave][lane], 16 B each
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RED + 2 * NW * 64 * 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rf = lane & 15, kq = lane >> 4;
+  const int nb = (p.N + 15) / 16;
+  const int G = gridDim.x;
+  if ((int)blockIdx.x >= nb) return;
+  const int my_blocks = (nb - (int)blockIdx.x + G - 1) / G;
+  const int nq = my_blocks * CPB;  // chunks of this workgroup
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, p.a_bytes);
+  auto ds_read16 = [&](uint32_t off) { return *(const i32x4*)(ring + off); };
+  auto ds_write16 = [&](uint32_t off, i32x4 v) { *(i32x4*)(ring + off) = v; };
+  // Barriers are bare s_barrier with the waits written out: __syncthreads() would also wait
+  // for every fill in flight (its fence orders the LDS-DMA writes too).
+
+  // fills: wave w moves rows 2 w and 2 w + 1 of a chunk, 1 KB (half a row) an instruction;
+  // lane l's 16 bytes land at piece 64 h + l of row r, which holds global piece
+  // (64 h + l) ^ (r % 16) of the row's 2 KB. The per-lane part of the address is
+  // loop-invariant; the block and the chunk go in the scalar offset.
+  uint32_t fv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 2 * wave + (i >> 1), h = i & 1;
+    fv[i] = (uint32_t)r * p.ldb_b + (uint32_t)(((64 * h + lane) ^ r) << 4);
+  }
+  auto fill = [&](int q) {
+    q = min(q, nq - 1);  // past the end: fetch the last chunk again (nothing reads it)
+    const int bi = (int)blockIdx.x + (q / CPB) * G, kc = q % CPB;
+    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u);
+    uint8_t* slot = ring + (q & (NR - 1)) * CH;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 2 * wave + (i >> 1), h = i & 1;
+      buf_load16_lds(rw, slot + r * 2048 + h * 1024, fv[i], so);
+    }
+  };
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  // the MFMAs of this wave's group of chunk q (its slot landed and visible)
+  auto mma = [&](int q, const i32x4 (&xc)[4]) {
+    const uint32_t slot = (uint32_t)(q & (NR - 1)) * CH;
+    i32x4 w[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int piece = 16 * wave + kq + 4 * s;  // global piece of the row in this chunk
+      w[s] = ds_read16(slot + rf * 2048 + ((piece ^ rf) << 4));
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[s]),
+                                                    __builtin_bit_cast(bf16x8, xc[s]), acc, 0, 0, 0);
+  };
+  // block j of this workgroup: its partial sums are at parity j & 1
+  auto finish = [&](int j) {
+    const int bi = (int)blockIdx.x + j * G;
+    i32x4 part[NW];
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) part[w2] = ds_read16(RED + (((j & 1) * NW + w2) * 64 + lane) * 16);
+    f32x4 sum = __builtin_bit_cast(f32x4, part[0]);
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) sum += __builtin_bit_cast(f32x4, part[w2]);
+    const int m = rf, n = bi * 16 + 4 * kq;
+    if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, fused_apply(p.ep, sum, m, n, true));
+  };
+
+  // X first: lane l holds row l % 16, 16 bytes at 16 (l / 16) + 64 s of K group
+  // 8 c + wave (chunk c's group of this wave), for k-steps s; then chunks 0-2 in flight.
+  // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed.
+  i32x4 x[CPB][4];
+#pragma unroll
+  for (int c = 0; c < CPB; ++c)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      x[c][s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * c + wave) * 256u);
+  fill(0);
+  fill(1);
+  fill(2);
+  __builtin_amdgcn_s_waitcnt(wait_vm_dec(12));
+  for (int j = 0; j < my_blocks; ++j) {
+#pragma unroll
+    for (int c = 0; c < CPB; ++c) {
+      const int q = j * CPB + c;
+      // chunk q landed (all but this wave's 8 newest loads: chunks q + 1, q + 2) and every
+      // wave is done with chunk q - 1, whose slot the fill of q + 3 takes
+      __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));  // and lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      fill(q + 3);
+      if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+      mma(q, x[c]);
+    }
+    ds_write16(RED + (((j & 1) * NW + wave) * 64 + lane) * 16, __builtin_bit_cast(i32x4, acc));
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last partial sums written
+  __builtin_amdgcn_s_barrier();
+  if (wave == 0) finish(my_blocks - 1);
+  __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // no fill lands in LDS after the exit
 }
 
 }  // namespace hkx

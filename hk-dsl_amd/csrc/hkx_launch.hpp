@@ -41,6 +41,10 @@ hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 g
 hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
                          hipStream_t s);
 
+// The streaming decode kernel (stream_kernel): M <= 16, K <= 4096, no split, unpaired.
+bool stream_takes(const DecodeArgs& a, int splits, bool pair);
+hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s);
+
 hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool program, dim3 grid,
                          hipStream_t s);
 

@@ -30,6 +30,9 @@ KERNEL_AUTO, KERNEL_TILE, KERNEL_DECODE = range(3)
 TILE_AUTO, TILE_PINGPONG, TILE_W4, TILE_W8, TILE_RING = range(5)
 PP_MFMA32, PP_ONE_TILE = 1, 2
 #: The tile schedules by name (the route candidates' "schedule").
+#: HKX_KERNEL_DECODE variant bit: the streaming kernel where it takes the call.
+DEC_STREAM = 1
+
 SCHEDULES = {"pp": TILE_PINGPONG, "w4": TILE_W4, "w8": TILE_W8, "ring": TILE_RING}
 
 OPS = ["MOV", "LOAD", "CONST", "ROW", "COL", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN",

@@ -54,7 +54,8 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},
     "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 4},
     "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 8},
-    "decode": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto"},
+    "decode": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto", "variant": 1},
+    "decode_blk": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto"},
     "decode_w4": {"kernel": "decode", "waves": 4, "rows": 16, "splits": "auto"},
     "decode_w16": {"kernel": "decode", "waves": 16, "rows": 16, "splits": "auto"},
 }
@@ -137,6 +138,10 @@ def resolve(rec: Dict[str, Any], m: int, n: int, k: int, fp8: bool = False) -> D
     """A candidate made concrete for a shape: the decode kernel's split over K (enough
     workgroups for twice the CUs, at least four 128-element groups a split)."""
     rec = dict(rec)
+    if rec["kernel"] == "decode" and rec.get("variant", 0) & 1 and m <= 16 and k <= 4096 \
+            and rec.get("splits") == "auto":
+        # the streaming kernel: one workgroup a CU walks all of W, no split
+        rec["splits"] = 1
     if rec["kernel"] == "decode" and rec.get("splits") == "auto":
         wgs = math.ceil(n / (16 * (rec.get("rows", 16) // 16)))
         groups = k // 128

@@ -433,8 +433,8 @@ class KernelDesc:
     sched: Dict[str, Any]
 
     def source(self) -> str:
-        return {"tile": "hk-dsl_amd/csrc/hkx_pp.hpp (ping-pong) / hkx_tile4.hpp (4 waves) / "
-                        "hkx_tile.hpp (8 waves)",
+        return {"tile": "hk-dsl_amd/csrc/hkx_ring.hpp (ring) / hkx_pp.hpp (ping-pong) / "
+                        "hkx_tile4.hpp (4 waves) / hkx_tile.hpp (8 waves)",
                 "decode": "hk-dsl_amd/csrc/hkx_decode.hpp",
                 "reduce": "hk-dsl_amd/csrc/hkx_reduce.hpp"}[self.name.split("<")[0]]
 
@@ -516,6 +516,7 @@ class _Launch:
             args.decode_waves = s.get("waves", 8)
             # the paired form needs each workgroup's gate and up fragments together
             args.decode_rows = 32 if ep.paired else s.get("rows", 16)
+            args.variant = s.get("variant", 0)
         args.splits = s.get("splits", 1)
         args.ep = ep.struct()
         self.args = args

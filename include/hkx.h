@@ -156,6 +156,10 @@ typedef struct HkxEpilogue {
 #define HKX_PP_MFMA32 1   /* 32 x 32 MFMA fragments (the fp8 and paired forms always use them) */
 #define HKX_PP_ONE_TILE 2 /* one tile a workgroup, instead of a grid of one workgroup a CU */
 
+/* HKX_KERNEL_DECODE variant bits. */
+#define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K <= 4096, no
+                             split, unpaired); other calls take the blocked kernel */
+
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */
   const void* b; /* (N, K) -- (2N, K) for HKX_EP_SILU_MUL -- row stride ldb elements */
@@ -171,7 +175,7 @@ typedef struct HkxGemmArgs {
   int32_t tile_schedule; /* TILE: HKX_TILE_*; AUTO = RING for 256 x 256 tiles it takes,
                             else PINGPONG for 256 x 256, else W4 where the tile takes it,
                             else W8 */
-  int32_t variant;  /* TILE, PINGPONG: HKX_PP_* bits (for tuning); 0 elsewhere */
+  int32_t variant;  /* TILE, PINGPONG: HKX_PP_* bits (for tuning); DECODE: HKX_DEC_* bits */
   int32_t decode_waves; /* DECODE: waves per workgroup (4, 8 or 16); 0 = default */
   int32_t decode_rows;  /* DECODE: W rows per workgroup (16 or 32); 0 = default */
   void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */

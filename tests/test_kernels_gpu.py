@@ -41,11 +41,13 @@ def _run(a, b, c, **kw):
     torch.cuda.synchronize()
 
 
-PP, W4, W8 = nat.TILE_PINGPONG, nat.TILE_W4, nat.TILE_W8
-SNAME = {PP: "pp", W4: "w4", W8: "w8"}
-#: (tile_m, tile_n, schedule, variant): the ping-pong kernel (16 x 16 and 32 x 32 MFMAs, one
-#: workgroup a CU or one a tile), the 4-wave (32 x 32 MFMA) and 8-wave (16 x 16) kernels
-TILES = [(256, 256, PP, 0), (256, 256, PP, nat.PP_MFMA32), (256, 256, PP, nat.PP_ONE_TILE),
+PP, W4, W8, RING = nat.TILE_PINGPONG, nat.TILE_W4, nat.TILE_W8, nat.TILE_RING
+SNAME = {PP: "pp", W4: "w4", W8: "w8", RING: "ring"}
+#: (tile_m, tile_n, schedule, variant): the ring kernel, the ping-pong kernel (16 x 16 and
+#: 32 x 32 MFMAs, one workgroup a CU or one a tile), the 4-wave (32 x 32 MFMA) and 8-wave
+#: (16 x 16) kernels
+TILES = [(256, 256, RING, 0), (256, 256, PP, 0), (256, 256, PP, nat.PP_MFMA32),
+         (256, 256, PP, nat.PP_ONE_TILE),
          (256, 256, W4, 0), (128, 256, W4, 0), (64, 256, W4, 0), (256, 256, W8, 0),
          (128, 256, W8, 0), (64, 256, W8, 0), (128, 128, W8, 0), (256, 128, W8, 0)]
 
@@ -70,7 +72,8 @@ def test_tile_plain_bf16(tile, shape):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP)], ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
+@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP), (256, RING)],
+                         ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
 @pytest.mark.parametrize("splits", [1, 2, 3, 4])
 def test_tile_bias_gelu_and_split(splits, tile):
     m, n, k = 200, 1408, 640
@@ -94,7 +97,7 @@ def test_tile_nothing_past_m():
     assert torch.equal(room[m:].cpu(), torch.full((8, n), 7.0, dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("sched", [(W4, 0), (W8, 0), (PP, 0), (PP, nat.PP_MFMA32)],
+@pytest.mark.parametrize("sched", [(W4, 0), (W8, 0), (PP, 0), (PP, nat.PP_MFMA32), (RING, 0)],
                          ids=lambda t: SNAME[t[0]] + str(t[1]))
 @pytest.mark.parametrize("out", [torch.float32, torch.float16])
 def test_tile_out_dtypes_residual_colscale(out, sched):
@@ -112,8 +115,8 @@ def test_tile_out_dtypes_residual_colscale(out, sched):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile", [(256, 256, PP), (256, 256, W4), (64, 256, W4), (256, 256, W8),
-                                  (128, 128, W8)], ids=tile_id)
+@pytest.mark.parametrize("tile", [(256, 256, RING), (256, 256, PP), (256, 256, W4), (64, 256, W4),
+                                  (256, 256, W8), (128, 128, W8)], ids=tile_id)
 def test_tile_fp8_scaled(tile):
     m, n, k = 300, 512, 1024
     g = torch.Generator().manual_seed(11)
@@ -154,7 +157,7 @@ def test_decode(m, cfg):
 
 @pytest.mark.parametrize("kernel", ["tile", "tile_split", "decode", "decode_split", "tile_fp32",
                                     "tile8", "tile8_split", "tilepp", "tilepp_split",
-                                    "tilepp_fp32"])
+                                    "tilepp_fp32", "tilering", "tilering_split", "tilering_fp32"])
 def test_silu_and_mul(kernel):
     m = 5 if kernel.startswith("decode") else 300
     n, k = 768, 512
@@ -170,8 +173,9 @@ def test_silu_and_mul(kernel):
         kw.update(kernel=nat.KERNEL_DECODE, decode_rows=32)
     else:
         kw.update(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
-                  schedule=W8 if kernel.startswith("tile8") else (PP if kernel.startswith("tilepp")
-                                                                  else W4))
+                  schedule=W8 if kernel.startswith("tile8") else (
+                      PP if kernel.startswith("tilepp") else (
+                          RING if kernel.startswith("tilering") else W4)))
     _run(a.to(DEV), b.to(DEV), c, **kw)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
@@ -211,7 +215,8 @@ def test_program_pass():
         O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP)], ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
+@pytest.mark.parametrize("tile", [(128, W4), (128, W8), (256, PP), (256, RING)],
+                         ids=lambda t: f"{t[0]}{SNAME[t[1]]}")
 def test_quantizing_stores(tile):
     m, n, k = 128, 512, 512
     a, b = _data(m, n, k, seed=12)
@@ -232,3 +237,80 @@ def test_quantizing_stores(tile):
     big = want.abs() > 16
     assert ((got - want).abs() / want.abs())[big].max().item() < 0.07
     assert got.abs().max().item() == 448.0
+
+
+# ---------------------------------------------------------------- the ring kernel's forms
+
+@pytest.mark.parametrize("act", [nat.ACT_NONE, nat.ACT_GELU_TANH, nat.ACT_SILU, nat.ACT_RELU])
+@pytest.mark.parametrize("shape", [(300, 1000, 512), (512, 768, 1024), (17, 264, 256)])
+def test_ring_bias_act(act, shape):
+    """The compiled bias + activation forms (bf16 bias vector, bf16 C), ragged M and N
+    (N % 256 != 0; N % 8 == 0), rows past M untouched."""
+    m, n, k = shape
+    a, b = _data(m, n, k, seed=21)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(22)) * 0.1).to(torch.bfloat16)
+    name = {nat.ACT_NONE: "bias", nat.ACT_GELU_TANH: "bias_gelu", nat.ACT_SILU: "bias_silu",
+            nat.ACT_RELU: "bias_relu"}[act]
+    acc = O.gemm_fp32(a, b) + bias.float()
+    ref = {"bias": acc, "bias_gelu": O.gelu_tanh(acc), "bias_silu": O.silu(acc),
+           "bias_relu": acc.clamp_min(0)}[name]
+    c = torch.full((m + 3, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    _run(a.to(DEV), b.to(DEV), c[:m], kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
+         schedule=RING, ep=_fused([(bd, nat.ROW)], ra=0, act=act))
+    O.assert_close(c[:m], ref, rtol=1e-2, atol=1e-2)
+    assert (c[m:].float() == 7.0).all()
+
+
+def test_ring_fp8_dequant_forms():
+    """fp8: the compiled dequant forms (fp32 column and row scales, with and without a
+    bf16 bias) and the generic one (a broadcast row scale), 2 x 3 tiles a workgroup."""
+    m, n, k = 600, 1280, 2048
+    g = torch.Generator().manual_seed(23)
+    a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    sa = (torch.rand(m, 1, generator=g) * 1.5 + 0.5) / 448
+    sb = (torch.rand(n, generator=g) * 1.5 + 0.5) / 448
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    _run(a8.to(DEV), b8.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
+         schedule=RING, ep=_fused([(sad, nat.COL), (sbd, nat.ROW)], cs=0, rs=1))
+    assert O.rel_to_max(c.cpu(), O.scaled_mm(a8, b8, sa, sb)) < 8e-3
+    _run(a8.to(DEV), b8.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
+         schedule=RING, ep=_fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)], cs=0, rs=1, ra=2))
+    O.assert_close(c, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+    one = torch.tensor([2.0 / 448], device=DEV)
+    ep = _fused([(sad, nat.COL), (one, nat.ROW)], cs=0, rs=1)
+    ep.ops[1].ld = 0  # one value for every column
+    _run(a8.to(DEV), b8.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
+         schedule=RING, ep=ep)
+    ref = O.gemm_fp32(a8.float(), b8.float()) * sa * (2.0 / 448)
+    assert O.rel_to_max(c.cpu(), ref) < 8e-3
+
+
+def test_ring_falls_back_for_ragged_n():
+    """N % 8 != 0 (a C the ring kernel cannot store in 16-byte pieces) runs on the
+    ping-pong kernel and is still right."""
+    m, n, k = 300, 1004, 512
+    a, b = _data(m, n, k, seed=24)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING)
+    O.assert_close(c, O.gemm_fp32(a, b), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024)])
+def test_decode_stream(m, nk):
+    """The streaming decode kernel (M <= 16, K a multiple of 1024 up to 4096): bias
+    epilogue, ragged N (rows of W past N read as zeros, columns past N never written)."""
+    n, k = nk
+    a, b = _data(m, n, k, seed=25)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(26)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias", O.gemm_fp32(a, b), bias=bias)
+    c = torch.full((m, n + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    _run(a.to(DEV), b.to(DEV), c[:, :n], kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+         ep=_fused([(bd, nat.ROW)], ra=0))
+    O.assert_close(c[:, :n], ref, rtol=1e-2, atol=1e-2)
+    assert (c[:, n:].float() == 7.0).all()
