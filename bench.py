@@ -13,7 +13,10 @@ dominant kernel (achieved TFLOP/s from HIP events around each launch, against th
 2.5 PFLOP/s bf16 dense peak), the CPU baseline (the oracle, torch fp32 on the host
 cores, on a bounded sample), and, under "also", the other BASELINE configs measured the
 same way: the fused gate_up + silu_and_mul GEMM, the decode GEMMs (HBM GB/s of W, with
-weight copies rotated past the 256 MB Infinity Cache) and the fp8 scaled GEMM.
+weight copies rotated past the 256 MB Infinity Cache; kernel time from a replayed graph,
+since a ~20 us launch is shorter than the host's per-call overhead) and the fp8 scaled
+GEMM. Before the warmup steps, each workload runs untimed for a quarter of a second: the
+GPU's clocks settle only after tens of milliseconds of load.
 """
 
 from __future__ import annotations
@@ -33,11 +36,29 @@ METRIC = "TFLOP/s & % MFMA peak (prefill M), HBM GB/s & % peak (decode M≤16)"
 PEAK_BF16, PEAK_FP8, PEAK_HBM = 2500.0, 5000.0, 8000.0
 
 
-def _events_time(fn, steps, warmup):
+def _ramp(fn, seconds=0.25):
+    """Untimed calls until `seconds` of device work have run: the GPU's clocks take tens of
+    milliseconds of load to settle (a 20 ms burst from idle runs ~15% slower than the same
+    burst after it), which a few warmup steps do not cover."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+RAMP_S = 0.25
+
+
+def _events_time(fn, steps, warmup, ramp=True):
     """Average device time of one call (HIP events on the current stream, which the
     kernels launch on) and the wall time of `steps` calls bracketed by synchronize."""
     import torch
 
+    if ramp and RAMP_S > 0:
+        _ramp(fn, RAMP_S)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -52,6 +73,36 @@ def _events_time(fn, steps, warmup):
     wall = time.perf_counter() - t0
     per = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
     return statistics.mean(per), statistics.median(per), wall
+
+
+def _graph_time(calls, reps=7):
+    """Device time of one call of `calls`, captured in one HIP graph and replayed (median of
+    `reps` replays): the kernel time of launches shorter than the host's call overhead."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ts.append(t0.elapsed_time(t1) * 1e-3 / len(calls))
+    return statistics.median(ts)
 
 
 def _inputs(m, k, n, seed, dev):
@@ -89,14 +140,18 @@ def cpu_baseline(x, wt, b):
 
 
 def main():
+    global RAMP_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="config 2 only, no CPU baseline")
+    ap.add_argument("--ramp", type=float, default=RAMP_S,
+                    help="seconds of untimed work before the warmup steps (0 under a profiler)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (the scale of rocprof's FETCH/WRITE_SIZE)")
     args = ap.parse_args()
+    RAMP_S = args.ramp
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not measured "
               f"(the GEMM shards over M or N with no exchange, or over K with one all-reduce "
@@ -141,10 +196,14 @@ def main():
                      "avg_launch_us": round(mean_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
                      "algorithmic_flops_per_launch": flops},
     }
-    tr = os.path.join(ROOT, "profiles", "traffic_tile_bias_gelu_cfg2.json")
+    # HBM bytes a launch of this kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # runs summarised under profiles/ (null if they were taken on another kernel)
+    tr = os.path.join(ROOT, "profiles", "traffic_ring_bias_gelu_cfg2.json")
     if os.path.isfile(tr):
         with open(tr) as f:
-            res["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+            rec = json.load(f)
+        if rec.get("kernel") == kname:
+            res["roofline"]["traffic"] = rec.get("hbm_bytes_per_launch")
     if not args.quick:
         res["also"] = other_configs(args.steps, args.warmup)
         del x, wt, b, out
@@ -181,24 +240,20 @@ def other_configs(steps, warmup):
                                               "frac_bf16_peak": round(fl / t / 1e12 / PEAK_BF16, 4),
                                               "us": round(t * 1e6, 1)}
         del x, wt, y
-    # config 4: decode, 4 weight copies (403 MB) rotated past the 256 MB MALL
+    # config 4: decode, 4 weight copies (403 MB) rotated past the 256 MB MALL; kernel time
+    # from a replayed graph of 32 calls
     ws = [_inputs(1, 4096, 12288, 40 + i, dev)[1] for i in range(4)]
     bias = _inputs(1, 4096, 12288, 4, dev)[2]
     for m in (1, 4, 16):
         x = _inputs(m, 4096, 12288, 4, dev)[0]
         for epi in ("plain", "bias"):
             y = torch.empty(m, 12288, device=dev, dtype=torch.bfloat16)
-            i = [0]
-
-            def call():
-                w = ws[i[0] % 4]
-                i[0] += 1
-                if epi == "bias":
-                    T(x, w, epilogue=T.bias, bias=bias, out=y)
-                else:
-                    T(x, w, out=y)
-
-            t, _, _ = _events_time(call, max(steps, 40), warmup)
+            if epi == "bias":
+                calls = [lambda w=ws[i % 4]: T(x, w, epilogue=T.bias, bias=bias, out=y) for i in range(32)]
+            else:
+                calls = [lambda w=ws[i % 4]: T(x, w, out=y) for i in range(32)]
+            # ~20 us launches: timed as a graph of 32 calls, the host's call overhead out
+            t = _graph_time(calls)
             byts = 12288 * 4096 * 2 + m * 4096 * 2 + m * 12288 * 2 + (12288 * 2 if epi == "bias" else 0)
             out[f"cfg4_decode_M{m}_{epi}"] = {"GB/s": round(byts / t / 1e9, 1),
                                               "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM, 4),
