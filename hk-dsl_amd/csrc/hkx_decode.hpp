@@ -167,7 +167,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 // gridDim.x-th), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
 // 1024 up to 1024 CPB.
 //
-// * W goes HBM -> LDS by buffer loads (`buffer_load_dwordx4 ... lds`), each instruction 1 KB
+// * W goes HBM -> LDS by non-temporal buffer loads (`buffer_load_dwordx4 ... lds`, read
+//   once, kept out of the caches), each instruction 1 KB
 //   of one row, contiguous -- the access a pure streaming read reaches HBM's ceiling with --
 //   in chunks of 16 rows x 1024 K (32 KB) through a ring of four: chunk q + 3 is in flight
 //   while chunk q is multiplied. A row's 128 16-byte pieces are stored XOR-swizzled by the
@@ -184,7 +185,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   constexpr int CH = 16 * 2048;  // a chunk: 16 rows x 2 KB
   constexpr int NR = 4;          // ring slots
   constexpr int RED = NR * CH;   // then the partial sums: [block parity][wave][lane], 16 B each
-  __shared__ __attribute__((aligned(16))) uint8_t ring[RED + 2 * NW * 64 * 16];
+  constexpr int EPV = RED + 2 * NW * 64 * 16;  // then the epilogue's vectors: [block % 3][cs, rs, ra][64 slots]
+  __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * 3 * 256];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -214,15 +216,63 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     fv[i] = (uint32_t)r * p.ldb_b + (uint32_t)(((64 * h + lane) ^ r) << 4);
   }
   auto fill = [&](int q) {
-    q = min(q, nq - 1);  // past the end: fetch the last chunk again (nothing reads it)
+    if (q >= nq) return;  // past the end: nothing (the waits count what was issued)
     const int bi = (int)blockIdx.x + (q / CPB) * G, kc = q % CPB;
     const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u);
     uint8_t* slot = ring + (q & (NR - 1)) * CH;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 2 * wave + (i >> 1), h = i & 1;
-      buf_load16_lds(rw, slot + r * 2048 + h * 1024, fv[i], so);
+      buf_load16_lds<kNonTemporal>(rw, slot + r * 2048 + h * 1024, fv[i], so);
     }
+  };
+  // The epilogue's vector operands of block j (row scale per token m, column scale and
+  // column add per output n) go global -> LDS by 4-byte DMA from wave 0, one block ahead,
+  // so they land under the waits the fills already have: a direct load in the epilogue
+  // would wait for every fill in flight (loads complete in order). Slot s of a vector
+  // holds the aligned 32-bit word that contains element s of the block (its 16-bit half
+  // picked by the element's address). Broadcast operands (stride 0) are read once.
+  const Fused& e = p.ep;
+  const bool fused = e.form == HKX_EP_FUSED;
+  const bool cs_vec = fused && e.cs.p && e.cs.ld, rs_vec = fused && e.rs.p && e.rs.ld,
+             ra_vec = fused && e.ra.p && e.ra.ld;
+  const float cs_sc = (fused && e.cs.p && !e.cs.ld) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : e.cmul;
+  const float rs_sc = (fused && e.rs.p && !e.rs.ld) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
+  const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
+  auto ep_load = [&](int j) {
+    if (wave != 0 || !(cs_vec || rs_vec || ra_vec)) return;
+    const int bi = (int)blockIdx.x + j * G;
+    uint8_t* base = ring + EPV + (j % 3) * 768;
+    const int l = lane;
+    constexpr uint32_t kOut = 0x7fffffffu;  // past every buffer's end: reads nothing
+    // the word of element idx, from the operand's address rounded down to 4 bytes (the
+    // bound rounded up: a dword only partly inside a buffer reads as zero)
+    auto load = [&](const Opnd& o, int64_t elems, bool ok, int64_t idx, uint8_t* dst) {
+      const uintptr_t a = (uintptr_t)o.p, al = a & ~(uintptr_t)3;
+      const uint32_t eb = o.dt == HKX_FP32 ? 4u : 2u;
+      const uint32_t byte = (uint32_t)(a - al) + (uint32_t)idx * eb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          make_rsrc((const void*)al, ((uint32_t)(a - al) + (uint32_t)elems * eb + 3u) & ~3u),
+          (__attribute__((address_space(3))) void*)dst, 4, ok ? (byte & ~3u) : kOut, 0, 0, 0);
+    };
+    const int n = bi * 16 + l;
+    if (cs_vec)
+      load(e.cs, (int64_t)(p.M - 1) * e.cs.ld + 1, l < 16 && l < p.M, (int64_t)l * e.cs.ld, base);
+    if (rs_vec) load(e.rs, p.N, l < 16 && n < p.N, n, base + 256);
+    if (ra_vec) load(e.ra, p.N, l < 16 && n < p.N, n, base + 512);
+  };
+  // which half of its word a 16-bit element is in (from its address)
+  auto hi_half = [](const Opnd& o, int64_t idx) {
+    return ((((uintptr_t)o.p >> 1) + (uint64_t)idx) & 1) != 0;
+  };
+  auto word_val = [](uint32_t w, int dt, bool hi) {
+    if (dt == HKX_FP32) return __builtin_bit_cast(float, w);
+    const uint32_t h = hi ? (w >> 16) : (w & 0xffffu);
+    return dt == HKX_FP16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : bf16_to_f32(h);
+  };
+  auto vec4 = [&](const uint32_t* s, const Opnd& o, int n) {
+    return f32x4{word_val(s[0], o.dt, hi_half(o, n)), word_val(s[1], o.dt, hi_half(o, n + 1)),
+                 word_val(s[2], o.dt, hi_half(o, n + 2)), word_val(s[3], o.dt, hi_half(o, n + 3))};
   };
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   // the MFMAs of this wave's group of chunk q (its slot landed and visible)
@@ -249,18 +299,30 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) sum += __builtin_bit_cast(f32x4, part[w2]);
     const int m = rf, n = bi * 16 + 4 * kq;
-    if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, fused_apply(p.ep, sum, m, n, true));
+    if (fused) {
+      const uint32_t* eo = (const uint32_t*)(ring + EPV + (j % 3) * 768);
+      const float cs = cs_vec ? word_val(eo[m], e.cs.dt, hi_half(e.cs, (int64_t)m * e.cs.ld)) * e.cmul
+                              : cs_sc;
+      const f32x4 rs = rs_vec ? vec4(eo + 64 + 4 * kq, e.rs, n) : f32x4{rs_sc, rs_sc, rs_sc, rs_sc};
+      const f32x4 ra = ra_vec ? vec4(eo + 128 + 4 * kq, e.ra, n) : f32x4{ra_sc, ra_sc, ra_sc, ra_sc};
+      sum = sum * (rs * cs) + ra;
+      if (e.ta.p && m < p.M && n < p.N) sum += ld_tile(e.ta, m, n);
+      sum = act4(e.act, sum + e.cadd);
+    }
+    if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
   };
 
   // X first: lane l holds row l % 16, 16 bytes at 16 (l / 16) + 64 s of K group
   // 8 c + wave (chunk c's group of this wave), for k-steps s; then chunks 0-2 in flight.
-  // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed.
+  // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed (with
+  // fewer than 3 chunks the first wait of the loop, which counts what was issued, sees to X).
   i32x4 x[CPB][4];
 #pragma unroll
   for (int c = 0; c < CPB; ++c)
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       x[c][s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * c + wave) * 256u);
+  ep_load(0);
   fill(0);
   fill(1);
   fill(2);
@@ -269,10 +331,14 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
 #pragma unroll
     for (int c = 0; c < CPB; ++c) {
       const int q = j * CPB + c;
-      // chunk q landed (all but this wave's 8 newest loads: chunks q + 1, q + 2) and every
-      // wave is done with chunk q - 1, whose slot the fill of q + 3 takes
-      __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));  // and lgkmcnt(0)
+      // chunk q landed (all but this wave's newest loads: the fills of chunks q + 1, q + 2,
+      // fewer at the end) and every wave is done with chunk q - 1, whose slot the fill of
+      // q + 3 takes; lgkmcnt(0) as well
+      if (q + 2 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
+      else if (q + 1 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
+      else __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
       __builtin_amdgcn_s_barrier();
+      if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);  // older than the fills of q + 3 on
       fill(q + 3);
       if (c == 0 && j > 0 && wave == 0) finish(j - 1);
       mma(q, x[c]);

@@ -43,9 +43,12 @@ HKX_DEV i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
 
 // 16 bytes a lane from global memory straight into LDS: lane l's bytes land at
 // lds + 16 l (the LDS base is wave-uniform; it goes in M0).
+// AUX is the cache policy: kNonTemporal marks a stream read once (kept out of the caches).
+constexpr int kNonTemporal = 2;
+template <int AUX = 0>
 HKX_DEV void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
-                                           voff, soff, 0, 0);
+                                           voff, soff, 0, AUX);
 }
 
 // ---------------------------------------------------------------- conversions
@@ -237,6 +240,23 @@ HKX_DEV f32x4 fused_apply(const Fused& e, f32x4 v, int m, int n, bool mvalid) {
   if (e.ta.p && mvalid) v += ld_tile(e.ta, m, n);
   v += e.cadd;
   return act4(e.act, v);
+}
+
+// Four epilogue operand values from LDS slots (one 32-bit slot per element: an fp32
+// value, or a 16-bit value in the low (even element) or high (odd element) half).
+HKX_DEV f32x4 slot4(const uint32_t* s, int dt) {
+  const i32x4 w = *(const i32x4*)s;
+  if (dt == HKX_FP32) return __builtin_bit_cast(f32x4, w);
+  const u32x2 pk = u32x2{((uint32_t)w.x & 0xffffu) | ((uint32_t)w.y & 0xffff0000u),
+                         ((uint32_t)w.z & 0xffffu) | ((uint32_t)w.w & 0xffff0000u)};
+  return dt == HKX_FP16 ? unpack_f16x4(pk) : unpack_bf16x4(pk);
+}
+
+HKX_DEV float slot1(const uint32_t* s, int e, int dt) {
+  const uint32_t w = s[e];
+  if (dt == HKX_FP32) return __builtin_bit_cast(float, w);
+  const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xffffu);
+  return dt == HKX_FP16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : bf16_to_f32(h);
 }
 
 HKX_DEV f32x4 silu_mul4(f32x4 g, f32x4 u) {

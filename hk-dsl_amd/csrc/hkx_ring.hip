@@ -34,6 +34,10 @@ bool ring_takes(const TileArgs& a, bool fp8, int mode) {
   // a 16-bit column scale is read as aligned pairs: unit stride only
   const Opnd& cs = a.ep.cs;
   if (a.ep.form == HKX_EP_FUSED && cs.p && cs.ld && cs.dt != HKX_FP32 && cs.ld != 1) return false;
+  // and from a 4-byte aligned address (the slot of an element is the aligned word it starts)
+  if (a.ep.form == HKX_EP_FUSED)
+    for (const Opnd* o : {&a.ep.cs, &a.ep.rs, &a.ep.ra})
+      if (o->p && o->ld && o->dt != HKX_FP32 && ((uintptr_t)o->p & 3)) return false;
   return true;
 }
 

@@ -53,23 +53,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int wait_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
-// Four epilogue operand values from LDS slots (one 32-bit slot per element: an fp32
-// value, or a 16-bit value in the low (even element) or high (odd element) half).
-HKX_DEV f32x4 slot4(const uint32_t* s, int dt) {
-  const i32x4 w = *(const i32x4*)s;
-  if (dt == HKX_FP32) return __builtin_bit_cast(f32x4, w);
-  const u32x2 pk = u32x2{((uint32_t)w.x & 0xffffu) | ((uint32_t)w.y & 0xffff0000u),
-                         ((uint32_t)w.z & 0xffffu) | ((uint32_t)w.w & 0xffff0000u)};
-  return dt == HKX_FP16 ? unpack_f16x4(pk) : unpack_bf16x4(pk);
-}
-
-HKX_DEV float slot1(const uint32_t* s, int e, int dt) {
-  const uint32_t w = s[e];
-  if (dt == HKX_FP32) return __builtin_bit_cast(float, w);
-  const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xffffu);
-  return dt == HKX_FP16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : bf16_to_f32(h);
-}
-
 // v_permlane32_swap: lanes 32-63 of a trade places with lanes 0-31 of b.
 HKX_DEV void swap32(uint32_t& a, uint32_t& b) {
   const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);

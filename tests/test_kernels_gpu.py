@@ -262,6 +262,21 @@ def test_ring_bias_act(act, shape):
     assert (c[m:].float() == 7.0).all()
 
 
+def test_ring_unaligned_col_scale_falls_back():
+    """A 16-bit per-token scale that starts 2 bytes into a word (a slice at an odd
+    element) is not the ring kernel's (its slots are aligned words): the 256 x 256 call
+    runs on the ping-pong kernel, with the same result."""
+    m, n, k = 300, 512, 256
+    a, b = _data(m, n, k, seed=29)
+    full = (torch.rand(m + 1, 1, generator=torch.Generator().manual_seed(30)) + 0.5).to(torch.float16)
+    ref = O.gemm_fp32(a, b) * full[1:].float()
+    fd = full.to(DEV)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256,
+         schedule=RING, ep=_fused([(fd[1:], nat.COL)], cs=0))
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
 def test_ring_fp8_dequant_forms():
     """fp8: the compiled dequant forms (fp32 column and row scales, with and without a
     bf16 bias) and the generic one (a broadcast row scale), 2 x 3 tiles a workgroup."""
@@ -300,7 +315,7 @@ def test_ring_falls_back_for_ragged_n():
 
 
 @pytest.mark.parametrize("m", [1, 4, 16])
-@pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024)])
+@pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024), (256, 1024), (4100, 3072)])
 def test_decode_stream(m, nk):
     """The streaming decode kernel (M <= 16, K a multiple of 1024 up to 4096): bias
     epilogue, ragged N (rows of W past N read as zeros, columns past N never written)."""
@@ -314,3 +329,27 @@ def test_decode_stream(m, nk):
          ep=_fused([(bd, nat.ROW)], ra=0))
     O.assert_close(c[:, :n], ref, rtol=1e-2, atol=1e-2)
     assert (c[:, n:].float() == 7.0).all()
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024)])
+def test_decode_stream_fused_forms(m, nk):
+    """The streaming decode kernel's whole fused form: a per-token scale with a stride (a
+    16-bit column of a wider tensor, odd elements in the high half of their word), a
+    per-channel fp32 scale, a bf16 column add, a residual tile, GELU -- the vectors staged
+    through LDS one block ahead."""
+    n, k = nk
+    a, b = _data(m, n, k, seed=27)
+    g = torch.Generator().manual_seed(28)
+    sa3 = (torch.rand(m, 3, generator=g) + 0.5).to(torch.float16)
+    sb = torch.rand(n, generator=g) + 0.5
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    acc = O.gemm_fp32(a, b)
+    ref = O.gelu_tanh(acc * sa3[:, 1:2].float() * sb * 0.5 + bias.float() + res.float() + 0.25)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    sa3d, sbd, bd, resd = sa3.to(DEV), sb.to(DEV), bias.to(DEV), res.to(DEV)
+    ep = _fused([(sa3d[:, 1:2], nat.COL), (sbd, nat.ROW), (bd, nat.ROW), (resd, nat.TILE)],
+                cs=0, rs=1, ra=2, ta=3, act=nat.ACT_GELU_TANH, cmul=0.5, cadd=0.25)
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM, ep=ep)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
