@@ -152,12 +152,27 @@ def stream_of(device) -> int:
 
 
 _WS: dict = {}
+#: Every workspace a captured CUDA graph has used: kept until the process ends.
+_PINNED: list = []
+
+
+def capturing(device) -> bool:
+    """Whether `device`'s current stream is capturing a CUDA graph."""
+    import torch  # noqa: PLC0415
+
+    return torch.cuda.is_current_stream_capturing()
 
 
 def workspace(device, nbytes: int):
     """A cached fp32 workspace of at least `nbytes` for (device, current stream): the
     reference's module-owned scratch (python/hk/ops/gemm_cdna_dp.py:330-338). Calls on
-    one stream run in order, so they can share it."""
+    one stream run in order, so they can share it.
+
+    Under CUDA-graph capture a graph bakes the buffer's address in, so a buffer a capture
+    has used is never freed: it is pinned for the life of the process (a bigger one for a
+    later call replaces it in the cache, not in memory). Otherwise a buffer replaced by a
+    bigger one is freed, and torch.cuda.graph's empty_cache() before the next capture can
+    unmap it under a graph that still replays it."""
     import torch  # noqa: PLC0415
 
     if nbytes == 0:
@@ -167,6 +182,8 @@ def workspace(device, nbytes: int):
     if buf is None or buf.numel() * 4 < nbytes:
         buf = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
         _WS[key] = buf
+    if capturing(device) and not any(b is buf for b in _PINNED):
+        _PINNED.append(buf)
     return buf
 
 

@@ -68,14 +68,27 @@ _TABLE: list = []
 
 
 def table() -> Dict[str, Dict[str, str]]:
-    """The measured table: {"NxK": {"M": candidate}} ($HK_GEMM_ROUTES names another)."""
+    """The measured table's routes: {"NxK": {"M": candidate}} ($HK_GEMM_ROUTES names
+    another file; `hk.integration.tune gemm` writes one). A table of another arch, or
+    naming a candidate this build does not have, is refused."""
     if not _TABLE:
         path = Path(os.environ.get("HK_GEMM_ROUTES", TABLE_PATH))
-        shapes = {}
+        routes = {}
         if path.is_file():
-            shapes = json.loads(path.read_text()).get("shapes", {})
-        _TABLE.append(shapes)
+            d = json.loads(path.read_text())
+            if d.get("arch", "gfx950") != "gfx950":
+                raise ValueError(f"{path} was measured on {d['arch']}, not gfx950")
+            routes = d.get("routes", {})
+            bad = {c for ent in routes.values() for c in ent.values()} - set(CANDIDATES)
+            if bad:
+                raise ValueError(f"{path} names candidates this build lacks: {sorted(bad)}")
+        _TABLE.append(routes)
     return _TABLE[0]
+
+
+def reload_table() -> None:
+    """Read the table again on the next route (after $HK_GEMM_ROUTES changes)."""
+    _TABLE.clear()
 
 
 def fits(name: str, m: int, n: int, k: int, fp8: bool = False) -> bool:
@@ -162,4 +175,5 @@ def matmul(a, b, out=None):
 
 
 __all__ = ["CANDIDATES", "OVERRIDE", "route", "rule", "resolve", "fits", "matmul", "table",
+           "reload_table",
            "K_STEP", "BLOCK_N_MIN", "CUS"]

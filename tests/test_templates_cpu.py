@@ -278,3 +278,27 @@ def test_shape_checks():
         T.plan(16, 4096, 100)
     with pytest.raises(ValueError, match="nothing to multiply"):
         T.plan(0, 4096, 4096)
+
+
+def test_workspace_used_under_capture_is_never_freed(monkeypatch):
+    """A workspace a graph capture used stays referenced after a bigger one replaces it in
+    the cache (a graph replays the address it captured)."""
+    from hk import _native as nat
+
+    monkeypatch.setattr(nat, "stream_of", lambda dev: 12345)
+    monkeypatch.setattr(nat, "_WS", {})
+    monkeypatch.setattr(nat, "_PINNED", [])
+    monkeypatch.setattr(nat, "capturing", lambda dev: True)
+    first = nat.workspace("cpu", 64)
+    assert nat.workspace("cpu", 32) is first
+    second = nat.workspace("cpu", 4096)
+    assert second is not first and second.numel() * 4 >= 4096
+    assert any(b is first for b in nat._PINNED) and any(b is second for b in nat._PINNED)
+    assert len(nat._PINNED) == 2
+    # outside capture, a replaced buffer is simply dropped
+    monkeypatch.setattr(nat, "capturing", lambda dev: False)
+    monkeypatch.setattr(nat, "_WS", {})
+    monkeypatch.setattr(nat, "_PINNED", [])
+    nat.workspace("cpu", 64)
+    nat.workspace("cpu", 4096)
+    assert nat._PINNED == []
