@@ -353,7 +353,12 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     arch = current_arch()
     shapes = model_shapes(args.models.split(","), args.tp)
     if args.kind == "gemm":
-        # the template's grid: the models' (N, K) and two squares (gemm_cdna_routes.py NK)
+        # the template's grid (gemm_cdna_routes.py NK): the models' (N, K), their gate and
+        # up projections unmerged, and two squares
+        for name in args.models.split(","):
+            cfg = MODELS[name] if name in MODELS else json.loads(Path(name).read_text())
+            cfg = cfg.get("text_config", cfg)
+            shapes.setdefault((cfg["intermediate_size"] // args.tp, cfg["hidden_size"]), "up")
         for sq in (4096, 8192):
             shapes.setdefault((sq, sq), "square")
     if args.only:

@@ -304,6 +304,19 @@ def test_ring_fp8_dequant_forms():
     assert O.rel_to_max(c.cpu(), ref) < 8e-3
 
 
+def test_ring_c_past_4gib_falls_back():
+    """C spanning 4 GiB or more (here a 512-column view of rows 2 MiB apart) is past the
+    ring kernel's 32-bit store offsets: the call runs on the ping-pong kernel, right to
+    the last row."""
+    m, n, k = 2100, 512, 256
+    a, b = _data(m, n, k, seed=31)
+    big = torch.empty((m, 1 << 20), dtype=torch.bfloat16, device=DEV)
+    c = big[:, :n]
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING)
+    O.assert_close(c, O.gemm_fp32(a, b), rtol=1e-2, atol=1e-2)
+    del big
+
+
 def test_ring_falls_back_for_ragged_n():
     """N % 8 != 0 (a C the ring kernel cannot store in 16-byte pieces) runs on the
     ping-pong kernel and is still right."""

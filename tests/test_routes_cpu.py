@@ -1,0 +1,100 @@
+"""The measured routing tables and the tuner's decisions, on the CPU.
+
+The decision rules restate python/hk/autotune/routes.py:92-272 (a kernel takes an M only
+where it beat the engine by min_gain; a tie stays the engine's; consecutive equal answers
+merge into runs; the answer at the largest M holds above it) and are checked here on
+hand-made points whose answers follow from the rule alone. The shipped tables are then
+checked against themselves: each route is what its own recorded points decide."""
+
+import json
+from pathlib import Path
+
+import pytest
+
+from hk.integration import engine, tune
+from hk.ops import gemm_cdna
+
+TUNED = Path(tune.__file__).resolve().parents[1] / "tuned"
+
+
+def test_base_path_needs_the_margin():
+    assert tune.base_path({"engine": 10.0, "hk": 9.0}) == "hk"          # 11% faster
+    assert tune.base_path({"engine": 10.0, "hk": 9.8}) == "fallback"    # 2% < 3%
+    assert tune.base_path({"engine": 10.0, "hk": 10.0}) == "fallback"   # a tie
+    assert tune.base_path({"engine": 10.0, "hk": 9.0, "hk_decode": 7.0}) == "hk_decode"
+    assert tune.base_path({"engine": 10.0}) == "fallback"
+    assert tune.base_path({"hk": 3.0}) == "hk"  # the engine failed its check
+    assert tune.base_path({"engine": 10.0, "hk": 9.8}, min_gain=0.01) == "hk"
+
+
+def test_runs_merge_and_answer_above():
+    pts = [[1, {"engine": 10, "hk_decode": 7}], [2, {"engine": 10, "hk_decode": 8}],
+           [4, {"engine": 10, "hk": 9.9}], [8, {"engine": 10, "hk": 8}], [16, {"engine": 10, "hk": 8}]]
+    rs, above = tune.runs(pts)
+    assert rs == [[1, 2, "hk_decode"], [4, 4, "fallback"], [8, 16, "hk"]] and above == "hk"
+    ent = tune.entry("x", pts, partial=True)
+    assert ent["above"] == "fallback" and ent["partial"]
+    t = engine.RouteTable({(64, 64): ent})
+    assert [t.lookup(m, 64, 64) for m in (1, 2, 3, 4, 8, 16, 32)] == \
+        ["hk_decode", "hk_decode", "fallback", "fallback", "hk", "hk", "fallback"]
+
+
+def test_linear_shapes_of_the_two_models():
+    q = {nm: (n, k) for nm, n, k, _ in tune.linear_shapes(tune.MODELS["Qwen/Qwen3-8B"])}
+    assert q == {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
+                 "down": (4096, 12288), "lm_head": (151936, 4096)}
+    ll = {nm: (n, k) for nm, n, k, _ in tune.linear_shapes(tune.MODELS["meta-llama/Meta-Llama-3-8B"])}
+    assert ll["gate_up"] == (28672, 4096) and ll["down"] == (4096, 14336)
+    assert ll["lm_head"] == (128256, 4096)
+    q2 = {nm: (n, k) for nm, n, k, _ in tune.linear_shapes(tune.MODELS["Qwen/Qwen3-8B"], tp=2)}
+    assert q2["qkv"] == (3072, 4096) and q2["down"] == (4096, 6144)
+
+
+def test_shipped_gemm_table_is_its_own_argmin():
+    d = json.loads((TUNED / "routes_gemm_gfx950.json").read_text())
+    assert d["arch"] == "gfx950"
+    assert set(d["candidates"]) == set(gemm_cdna.CANDIDATES)
+    for p in d["points"]:
+        hk_us = {c[3:]: v for c, v in p["us"].items() if c.startswith("hk:")}
+        assert d["routes"][f"{p['n']}x{p['k']}"][str(p["m"])] == min(hk_us, key=hk_us.get)
+    # the models' shapes and the config-2 / config-4 shape are all measured
+    for nk in ("6144x4096", "4096x4096", "24576x4096", "4096x12288", "151936x4096",
+               "28672x4096", "4096x14336", "128256x4096", "12288x4096"):
+        assert nk in d["routes"], nk
+
+
+def test_gemm_route_reads_the_table(monkeypatch):
+    monkeypatch.setattr(gemm_cdna, "OVERRIDE", {})
+    gemm_cdna.reload_table()
+    routes = gemm_cdna.table()
+    assert routes["12288x4096"]["4096"] == gemm_cdna.route(4096, 12288, 4096)
+    # the nearest measured M on a log scale
+    assert gemm_cdna.route(3000, 12288, 4096) == routes["12288x4096"]["4096"]
+    # an unmeasured shape takes the rule
+    assert gemm_cdna.route(4096, 12344, 4096) == gemm_cdna.rule(4096, 12344, 4096)
+
+
+def test_a_table_naming_unknown_candidates_is_refused(tmp_path, monkeypatch):
+    bad = tmp_path / "r.json"
+    bad.write_text(json.dumps({"arch": "gfx950", "routes": {"64x64": {"1": "nope"}}}))
+    monkeypatch.setenv("HK_GEMM_ROUTES", str(bad))
+    gemm_cdna.reload_table()
+    with pytest.raises(ValueError, match="nope"):
+        gemm_cdna.table()
+    monkeypatch.delenv("HK_GEMM_ROUTES")
+    gemm_cdna.reload_table()
+
+
+def test_shipped_vllm_table_is_its_own_decision():
+    path = TUNED / "routes_vllm_linear_gfx950.json"
+    d = json.loads(path.read_text())
+    assert d["arch"] == "gfx950" and d["min_gain"] == tune.MIN_GAIN
+    t = engine.RouteTable.from_json(path)
+    for key, ent in d["shapes"].items():
+        rs, above = tune.runs(ent["points"], d["min_gain"])
+        assert ent["runs"] == rs, key
+        n, k = (int(v) for v in key.split("x"))
+        for m, times in ent["points"]:
+            assert t.lookup(m, n, k) == tune.base_path(times, d["min_gain"])
+    # decode-sized M on the K = 4096 shapes goes to the decode kernel
+    assert t.lookup(1, 4096, 4096) == "hk_decode" and t.lookup(16, 24576, 4096) == "hk_decode"
