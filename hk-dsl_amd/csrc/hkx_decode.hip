@@ -45,7 +45,7 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
 
 bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
   const int groups = a.g_total;  // 128-element K groups
-  return splits == 1 && !pair && a.M <= 16 && groups % 8 == 0 && groups <= 32;
+  return splits == 1 && !pair && a.M <= 16 && groups % 8 == 0 && groups <= 256;
 }
 
 hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s) {
@@ -55,7 +55,7 @@ hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s) {
     case 2: hipLaunchKernelGGL((stream_kernel<2>), grid, block, 0, s, a); break;
     case 3: hipLaunchKernelGGL((stream_kernel<3>), grid, block, 0, s, a); break;
     case 4: hipLaunchKernelGGL((stream_kernel<4>), grid, block, 0, s, a); break;
-    default: return hipErrorInvalidValue;
+    default: hipLaunchKernelGGL((stream_kernel<0>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }

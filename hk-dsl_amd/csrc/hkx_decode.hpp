@@ -165,7 +165,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 
 // The streaming decode GEMM: one workgroup a CU walks the 16-row blocks of W (every
 // gridDim.x-th), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
-// 1024 up to 1024 CPB.
+// 1024: CPB chunks of 1024 a block (CPB = 1..4), or, with CPB = 0, K / 1024 of them read
+// at run time (K past 4096).
 //
 // * W goes HBM -> LDS by non-temporal buffer loads (`buffer_load_dwordx4 ... lds`, read
 //   once, kept out of the caches), each instruction 1 KB
@@ -175,7 +176,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 //   row (piece c at c ^ (r % 16)), applied on the global side, so the MFMA fragment reads
 //   (16 rows, one piece each) are conflict-free.
 // * X is the same for every block: wave w owns the 128-element group w of every chunk, and
-//   loads its share of X (CPB groups of 16 rows) into registers once.
+//   loads its share of X (CPB groups of 16 rows) into registers once; past K = 4096 it is
+//   streamed with the chunks instead (two chunks ahead, three register slots).
 // * v_mfma_f32_16x16x32_bf16 with W's fragment first; the 8 waves' partial sums of a block
 //   meet in LDS (double-buffered by block parity), and wave 0 sums, applies the epilogue and
 //   stores after the next chunk's barrier, under the other waves' MFMAs.
@@ -196,7 +198,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const int G = gridDim.x;
   if ((int)blockIdx.x >= nb) return;
   const int my_blocks = (nb - (int)blockIdx.x + G - 1) / G;
-  const int nq = my_blocks * CPB;  // chunks of this workgroup
+  const int cpb = CPB ? CPB : p.g_total / 8;  // chunks a block
+  const int nq = my_blocks * cpb;             // chunks of this workgroup
 
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, p.a_bytes);
@@ -217,7 +220,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   }
   auto fill = [&](int q) {
     if (q >= nq) return;  // past the end: nothing (the waits count what was issued)
-    const int bi = (int)blockIdx.x + (q / CPB) * G, kc = q % CPB;
+    const int jb = q / cpb, kc = q - jb * cpb;
+    const int bi = (int)blockIdx.x + jb * G;
     const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u);
     uint8_t* slot = ring + (q & (NR - 1)) * CH;
 #pragma unroll
@@ -312,39 +316,83 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
   };
 
-  // X first: lane l holds row l % 16, 16 bytes at 16 (l / 16) + 64 s of K group
-  // 8 c + wave (chunk c's group of this wave), for k-steps s; then chunks 0-2 in flight.
-  // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed (with
-  // fewer than 3 chunks the first wait of the loop, which counts what was issued, sees to X).
-  i32x4 x[CPB][4];
-#pragma unroll
-  for (int c = 0; c < CPB; ++c)
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      x[c][s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * c + wave) * 256u);
-  ep_load(0);
-  fill(0);
-  fill(1);
-  fill(2);
-  __builtin_amdgcn_s_waitcnt(wait_vm_dec(12));
-  for (int j = 0; j < my_blocks; ++j) {
-#pragma unroll
-    for (int c = 0; c < CPB; ++c) {
-      const int q = j * CPB + c;
-      // chunk q landed (all but this wave's newest loads: the fills of chunks q + 1, q + 2,
-      // fewer at the end) and every wave is done with chunk q - 1, whose slot the fill of
-      // q + 3 takes; lgkmcnt(0) as well
-      if (q + 2 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
-      else if (q + 1 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
-      else __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
-      __builtin_amdgcn_s_barrier();
-      if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);  // older than the fills of q + 3 on
-      fill(q + 3);
-      if (c == 0 && j > 0 && wave == 0) finish(j - 1);
-      mma(q, x[c]);
-    }
+  // chunk q landed (all but this wave's newest loads: those of chunks q + 1 and q + 2,
+  // fewer at the end) and every wave is done with chunk q - 1, whose slot the fill of
+  // q + 3 takes; lgkmcnt(0) as well
+  auto wait_chunk = [&](int q) {
+    if (q + 2 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
+    else if (q + 1 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
+    else __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
+  };
+  auto block_done = [&](int j) {
     ds_write16(RED + (((j & 1) * NW + wave) * 64 + lane) * 16, __builtin_bit_cast(i32x4, acc));
     acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  // lane l's share of X for chunk c: row l % 16, 16 bytes at 16 (l / 16) + 64 s of K group
+  // 8 c + wave (chunk c's group of this wave), for k-steps s
+  auto xload = [&](int c, i32x4 (&dst)[4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      dst[s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * c + wave) * 256u);
+  };
+
+  if constexpr (CPB > 0) {
+    // X held in registers for the whole walk, loaded first; then chunks 0-2 in flight.
+    // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed
+    // (with fewer than 3 chunks the first wait of the loop, which counts what was issued,
+    // sees to X).
+    i32x4 x[CPB][4];
+#pragma unroll
+    for (int c = 0; c < CPB; ++c) xload(c, x[c]);
+    ep_load(0);
+    fill(0);
+    fill(1);
+    fill(2);
+    __builtin_amdgcn_s_waitcnt(wait_vm_dec(12));
+    for (int j = 0; j < my_blocks; ++j) {
+#pragma unroll
+      for (int c = 0; c < CPB; ++c) {
+        const int q = j * CPB + c;
+        wait_chunk(q);
+        __builtin_amdgcn_s_barrier();
+        if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);  // older than the fills of q + 3 on
+        fill(q + 3);
+        if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+        mma(q, x[c]);
+      }
+      block_done(j);
+    }
+  } else {
+    // K past 4096: X streamed with the chunks, two ahead, through three register slots
+    // (the loop is unrolled by three so every slot is a fixed register set). A chunk's X
+    // loads follow the fill of the chunk three ahead, so the loads issued after chunk q's
+    // are again those of chunks q + 1 and q + 2, and the same waits hold.
+    i32x4 xs[3][4];
+    auto xnext = [&](int q, i32x4 (&dst)[4]) {
+      if (q < nq) xload(q % cpb, dst);
+    };
+    ep_load(0);
+    fill(0);
+    fill(1);
+    xnext(0, xs[0]);
+    fill(2);
+    xnext(1, xs[1]);
+    auto step = [&](int q, const i32x4 (&xc)[4], i32x4 (&xn)[4]) {
+      const int j = q / cpb, c = q - j * cpb;
+      wait_chunk(q);
+      __builtin_amdgcn_s_barrier();
+      if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);
+      fill(q + 3);
+      xnext(q + 2, xn);
+      if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+      mma(q, xc);
+      if (c == cpb - 1) block_done(j);
+    };
+    for (int q = 0; q < nq; q += 3) {
+      step(q, xs[0], xs[2]);
+      if (q + 1 < nq) step(q + 1, xs[1], xs[0]);
+      if (q + 2 < nq) step(q + 2, xs[2], xs[1]);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last partial sums written
   __builtin_amdgcn_s_barrier();

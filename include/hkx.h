@@ -157,8 +157,9 @@ typedef struct HkxEpilogue {
 #define HKX_PP_ONE_TILE 2 /* one tile a workgroup, instead of a grid of one workgroup a CU */
 
 /* HKX_KERNEL_DECODE variant bits. */
-#define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K <= 4096, no
-                             split, unpaired); other calls take the blocked kernel */
+#define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K a multiple
+                             of 1024 up to 32768, no split, unpaired); other calls take the
+                             blocked kernel */
 
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */

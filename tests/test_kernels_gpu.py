@@ -328,10 +328,12 @@ def test_ring_falls_back_for_ragged_n():
 
 
 @pytest.mark.parametrize("m", [1, 4, 16])
-@pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024), (256, 1024), (4100, 3072)])
+@pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024), (256, 1024), (4100, 3072),
+                                (4096, 12288), (1000, 14336), (300, 5120), (16, 6144)])
 def test_decode_stream(m, nk):
-    """The streaming decode kernel (M <= 16, K a multiple of 1024 up to 4096): bias
-    epilogue, ragged N (rows of W past N read as zeros, columns past N never written)."""
+    """The streaming decode kernel (M <= 16, K a multiple of 1024; past 4096 X is streamed
+    with the chunks): bias epilogue, ragged N (rows of W past N read as zeros, columns
+    past N never written), chunk counts per workgroup from 1 up (3 ahead of the ring)."""
     n, k = nk
     a, b = _data(m, n, k, seed=25)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(26)).to(torch.bfloat16)
@@ -345,7 +347,7 @@ def test_decode_stream(m, nk):
 
 
 @pytest.mark.parametrize("m", [1, 7, 16])
-@pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024)])
+@pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024), (1000, 6144)])
 def test_decode_stream_fused_forms(m, nk):
     """The streaming decode kernel's whole fused form: a per-token scale with a stride (a
     16-bit column of a wider tensor, odd elements in the high half of their word), a
