@@ -480,6 +480,68 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
   return HKX_OK;
 }
 
+int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const uint8_t* sa,
+                int64_t sa_ld, const uint8_t* sb, int64_t sb_ld, void* c, int64_t ldc, int32_t m,
+                int32_t n, int32_t k, void* stream) {
+  g_err.clear();
+  if (!a || !b || !c || !sa || !sb) return fail(HKX_ERR_ARG, "mx_gemm: a null pointer");
+  if (m < 1 || n < 1 || k < 1) return fail(HKX_ERR_SHAPE, "mx_gemm: M=%d N=%d K=%d", m, n, k);
+  if (k % 128 || n % 8)
+    return fail(HKX_ERR_SHAPE, "mx_gemm: K=%d must be a multiple of 128 and N=%d of 8", k, n);
+  if (lda < k || ldb < k || ldc < n || sa_ld < k / 32 || sb_ld < k / 32)
+    return fail(HKX_ERR_SHAPE, "mx_gemm: row strides below K, N or K/32");
+  if (!aligned(a, 16) || !aligned(b, 16) || lda % 16 || ldb % 16)
+    return fail(HKX_ERR_SHAPE, "mx_gemm: A and B need 16-byte aligned rows");
+  if (!aligned(c, 16) || (ldc * 2) % 16)
+    return fail(HKX_ERR_SHAPE, "mx_gemm: C (bf16) needs 16-byte aligned rows");
+  if (!aligned(sa, 4) || !aligned(sb, 4) || sa_ld % 4 || sb_ld % 4)
+    return fail(HKX_ERR_SHAPE, "mx_gemm: the scales need 4-byte aligned rows");
+  if ((long long)m * lda >= (1LL << 32) || (long long)n * ldb >= (1LL << 32) ||
+      (long long)m * ldc * 2 >= (1LL << 32))
+    return fail(HKX_ERR_SHAPE, "mx_gemm: A, B or C spans 4 GiB or more; split the call");
+  hkx::TileArgs t{};
+  t.a = a;
+  t.b = b;
+  t.c = c;
+  t.a_bytes = (uint32_t)((long long)m * lda);
+  t.b_bytes = (uint32_t)((long long)n * ldb);
+  t.lda_b = (uint32_t)lda;
+  t.ldb_b = (uint32_t)ldb;
+  t.ldc = ldc;
+  t.M = m;
+  t.N = n;
+  t.kt_total = t.kt_split = k / 128;
+  t.tiles_m = (m + 255) / 256;
+  t.tiles_n = (n + 255) / 256;
+  t.wgm = kWgmRows;
+  t.pair_off = n;
+  t.c_dt = HKX_BF16;
+  t.c_aligned = 1;
+  t.ep.form = HKX_EP_NONE;
+  t.ep.cmul = 1.0f;
+  t.sa = sa;
+  t.sb = sb;
+  t.sa_ld = (uint32_t)sa_ld;
+  t.sb_ld = (uint32_t)sb_ld;
+  t.sa_bytes = (uint32_t)((long long)m * sa_ld);
+  t.sb_bytes = (uint32_t)((long long)n * sb_ld);
+  const dim3 g(std::min(t.tiles_m * t.tiles_n, cu_count()));
+  return launched(hkx::launch_ring_mx(t, g, (hipStream_t)stream), "mx GEMM");
+}
+
+int hkx_mx_quant(const void* x, int64_t ldx, void* q, int64_t ldq, uint8_t* s, int64_t lds,
+                 int32_t m, int32_t k, void* stream) {
+  g_err.clear();
+  if (!x || !q || !s) return fail(HKX_ERR_ARG, "mx_quant: a null pointer");
+  if (m < 0 || k < 0 || k % 32) return fail(HKX_ERR_SHAPE, "mx_quant: K=%d, a multiple of 32", k);
+  if (ldx < k || ldq < k || lds < k / 32) return fail(HKX_ERR_SHAPE, "mx_quant: row strides");
+  if (!aligned(x, 16) || ldx % 8 || !aligned(q, 8) || ldq % 8)
+    return fail(HKX_ERR_SHAPE, "mx_quant: x needs 16-byte and q 8-byte aligned rows");
+  if (m == 0 || k == 0) return HKX_OK;
+  return launched(hkx::launch_mx_quant(x, ldx, q, ldq, s, lds, m, k, (hipStream_t)stream),
+                  "mx quant");
+}
+
 int hkx_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
                   int64_t sa_ld, const float* scale_b, int32_t sb_per_channel, const void* bias,
                   void* c, int64_t ldc, int32_t m, int32_t n, int32_t k, void* ws,

@@ -74,7 +74,7 @@ constexpr int kEpDeq = 2;      // act(acc cs[m] rs[n]), cs and rs fp32
 constexpr int kEpDeqBias = 3;  // act(acc cs[m] rs[n] + ra[n]), cs and rs fp32, ra bf16
 constexpr int kEpGeneric = 4;  // the whole fused form with run-time types and output type
 
-template <bool FP8, int MODE, int ACT, int EPF>
+template <bool FP8, int MODE, int ACT, int EPF, bool MX = false>
 __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   constexpr int BM = 256, BN = 256;
   constexpr int FR = FP8 ? 32 : 16;           // fragment edge
@@ -82,7 +82,10 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   constexpr int HS = 512 * 64;                 // one half-stage buffer
   constexpr int NBUF = 4;
   constexpr int EPO = NBUF * HS;  // epilogue operands: [tile parity][cs, rs, ra][256 slots]
-  constexpr int SMEM = EPO + 2 * 3 * 1024;
+  constexpr int SCO = EPO + 2 * 3 * 1024;  // MX scales: [ring slot][512 rows] of 4 bytes
+  constexpr int SMEM = SCO + (MX ? NBUF * 2048 : 0);
+  static_assert(!MX || FP8, "MX scales go with fp8 operands");
+  constexpr int NV = MX ? 5 : 4;  // vector-memory operations a wave's fill of a half-stage makes
   constexpr bool PAIR = (MODE == kPair16 || MODE == kPairWs);
   constexpr int OUTW = PAIR ? BN / 2 : BN;
   static_assert(!(PAIR && FP8) && !(MODE == kStore8 && PAIR), "modes");
@@ -141,10 +144,17 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   uint32_t fa = 0, fb = 0;
   const uint32_t sa_step = 128u * p.lda_b, sb_step = (PAIR ? 64u : 128u) * p.ldb_b;
   int f_lt = 0, f_kv = 0, f_u = 0;  // the next fill: local tile, half-stage in it, global
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(MX ? p.sa : nullptr, MX ? p.sa_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(MX ? p.sb : nullptr, MX ? p.sb_bytes : 0u);
+  uint32_t fsa = 0, fsb = 0;  // this lane's scale row (MX)
   auto fill_tile = [&](int lt) {
     int m0, n0;
     tile_at(lt, m0, n0);
     const int ln = opaque_lane();
+    if constexpr (MX) {
+      fsa = (uint32_t)(m0 + 64 * (wave & 3) + ln) * p.sa_ld;
+      fsb = (uint32_t)(n0 + 64 * (wave & 3) + ln) * p.sb_ld;
+    }
     const int r = 16 * wave + (ln >> 2);  // row of instruction 0 (A), 2 (B, less 256)
     const uint32_t ch = (uint32_t)(((ln & 3) ^ swz4(r)) << 4);
     fa = (uint32_t)(m0 + r) * p.lda_b + ch;
@@ -167,6 +177,14 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
     for (int i = 0; i < 4; ++i)
       buf_load16_lds(i < 2 ? ra : rb, base + i * 8192, i < 2 ? fa : fb,
                      so + (uint32_t)(i & 1) * (i < 2 ? sa_step : sb_step));
+    if constexpr (MX) {
+      // the E8M0 scales of this half-stage's 64 K (blocks 2 uk and 2 uk + 1 of 32): lane l
+      // of wave w takes the aligned dword that holds them for row 64 w + l (A rows, then B)
+      const uint32_t uk = (uint32_t)(2 * kt0 + f_kv);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wave < 4 ? rsa : rsb,
+          (__attribute__((address_space(3))) void*)(smem + SCO + (f_u & (NBUF - 1)) * 2048 + wave * 256),
+          4, wave < 4 ? fsa : fsb, __builtin_amdgcn_readfirstlane(4u * (uk >> 1)), 0, 0);
+    }
     ++f_u;
     if (f_u < nu) {
       if (++f_kv == hpt) {
@@ -215,21 +233,40 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
 
   // ---- fragment reads. 16 x 16 bf16: lane l reads row l % 16 of a fragment, chunk l / 16
   // (a 16-row fragment's swizzle bit 4 is the fragment's parity: rdo[1] serves the odd
-  // ones). 32 x 32 fp8: lane l reads row l % 32, chunks 2 (l / 32) and + 1.
+  // ones). 32 x 32 fp8: lane l reads row l % 32, chunks l / 32 and 2 + l / 32: the scaled
+  // MFMA takes a lane's bytes 0-15 as K block 0 of its 64 and bytes 16-31 as block 1 (the
+  // scale of block b coming from the lanes l / 32 = b), so lane half h holds K [16 h, +16)
+  // of each 32-K block.
   uint32_t rdo[2];
   {
     const int rf = lane & (FR - 1), h = lane / FR;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int lc = FP8 ? (2 * h + q) : h;
+      const int lc = FP8 ? (2 * q + h) : h;
       const int sw = swz4(FP8 ? rf : rf + 16 * q);
       rdo[q] = rf * 64 + ((lc ^ sw) << 4);
     }
   }
   constexpr int FB = FR * 64;  // bytes of a fragment's rows in a buffer
   const int a_off = row0 * 64, b_off = (BM + col0) * 64;
+  // MX: lanes l / 32 = h give the scale of 32-K block h of the MFMA's 64 for their fragment
+  // row: byte 2 (uk & 1) + h of the row's dword (uk: the half-stage's place in K, whose
+  // parity is u's), shifted down to byte 0, the MFMA's scale select
+  uint32_t sfa[FM], sfb[FN];
+  const int sc_sh = 8 * (lane >> 5);
+  auto read_scales = [&](int u) {
+    if constexpr (MX) {
+      const uint32_t* sc = (const uint32_t*)(smem + SCO + (u & (NBUF - 1)) * 2048);
+      const int rf = lane & 31, sh = sc_sh + 16 * (u & 1);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) sfb[j] = sc[BM + col0 + 32 * j + rf] >> sh;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) sfa[i] = sc[row0 + 32 * i + rf] >> sh;
+    }
+  };
   auto read_frags = [&](int u, Frag (&af)[FM], Frag (&bf)[FN]) {
     const uint8_t* s = smem + (u & (NBUF - 1)) * HS;
+    read_scales(u);
     if constexpr (FP8) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -258,7 +295,10 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const Acc c = decltype(zero)::value ? Acc{} : acc[i][j];
-        if constexpr (FP8)
+        if constexpr (MX)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, 0, 0, 0,
+                                                                     (int)sfb[j], 0, (int)sfa[i]);
+        else if constexpr (FP8)
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, 0, 0, 0, 0,
                                                                      0, 0);
         else
@@ -423,7 +463,7 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   fill_next();
   fill_next();
   fill_next();
-  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // this wave's share of half-stage 0 landed
+  __builtin_amdgcn_s_waitcnt(wait_vm(2 * NV));  // this wave's share of half-stage 0 landed
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();
   int u = 0;
@@ -433,7 +473,7 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
       read_frags(u, af, bf);
       if (k == 0 && lt + 1 < my_tiles) ep_load(lt + 1);
       fill_next();
-      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * NV));
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -443,7 +483,7 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
       else mma(af, bf, std::false_type{});
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(wait_vm(8));
+      __builtin_amdgcn_s_waitcnt(wait_vm(2 * NV));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     }

@@ -48,6 +48,12 @@ struct TileArgs {
   int32_t c_dt;
   int32_t c_aligned;   // C's rows are 16-byte aligned: whole-chunk stores
   Fused ep;
+  // MX block scales (the ring kernel's MX form): E8M0 bytes, one a row and 32 K, row
+  // strides in bytes; bounds in bytes for the buffer resources
+  const uint8_t* sa;
+  const uint8_t* sb;
+  uint32_t sa_ld, sb_ld;
+  uint32_t sa_bytes, sb_bytes;
 };
 
 // How a tile leaves the kernel.

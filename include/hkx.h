@@ -25,6 +25,14 @@
  *                       decode_gemm_kernel (python/hk/ops/decode_gemm.py:37-180).
  *   hkx_scaled_mm       hk.ops.gemm.scaled_mm's launch (python/hk/ops/gemm.py:884-975):
  *                       bf16 (A . B^T) * scale_a * scale_b (+ bias), fp8 operands.
+ *   hkx_mx_gemm         hk.ops.mxfp8.gemm / gemm_pp's launch (python/hk/ops/mxfp8.py:64-110,
+ *                       gemm_cdna.gemm_kernel with mx=True, python/hk/ops/gemm_cdna.py:82-94):
+ *                       bf16 C = (sa . A)(sb . B)^T, fp8-e4m3 operands with OCP MX E8M0
+ *                       scales, one byte a row and 32 K.
+ *   hkx_mx_quant        hk.ops.mxfp8.quant's launch (python/hk/ops/mxfp8.py:605-660): bf16
+ *                       rows to fp8-e4m3 with an E8M0 scale a 32-column block, AITER's
+ *                       per_1x32 rule (python/hk/mx.py:17-31), the scales in the OCP
+ *                       layout the MX GEMM reads.
  *   hkx_gemm_workspace  gemm_cdna_dp.scratch_for / decode_gemm.scratch_for
  *                       (gemm_cdna_dp.py:330-338, decode_gemm.py:283-298): the size of
  *                       the fp32 share buffer a plan needs (the caller allocates it).
@@ -213,6 +221,22 @@ int hkx_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                   int32_t sb_per_channel, const void* bias, void* c, int64_t ldc,
                   int32_t m, int32_t n, int32_t k, void* ws, size_t ws_bytes,
                   void* stream);
+
+/* bf16 C = (sa . A)(sb . B)^T: A (M, K) and B (N, K) fp8-e4m3, sa (M, K/32) and sb
+ * (N, K/32) E8M0 bytes (scale 2^(s - 127) for its row and 32 K), row strides lda, ldb,
+ * ldc in elements and sa_ld, sb_ld in bytes. K a multiple of 128, N of 8; sa and sb
+ * 4-byte aligned with sa_ld, sb_ld multiples of 4 and >= K/32; C's rows 16-byte aligned.
+ * M any. */
+int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const uint8_t* sa,
+                int64_t sa_ld, const uint8_t* sb, int64_t sb_ld, void* c, int64_t ldc,
+                int32_t m, int32_t n, int32_t k, void* stream);
+
+/* x bf16 (M, K) -> q fp8-e4m3 (M, K) and s (M, K/32) E8M0 bytes: per 32-column block,
+ * e = ceil(log2(amax / 448)) with amax >= 2^-126, q = x / 2^e rounded to nearest even,
+ * s = clamp(e + 127, 0, 254). K a multiple of 32; row strides in elements (bytes for
+ * q and s). */
+int hkx_mx_quant(const void* x, int64_t ldx, void* q, int64_t ldq, uint8_t* s, int64_t lds,
+                 int32_t m, int32_t k, void* stream);
 
 #ifdef __cplusplus
 }

@@ -197,3 +197,35 @@ def assert_close(got: torch.Tensor, ref: torch.Tensor, rtol: float, atol: float)
 __all__ = ["gelu_tanh", "gelu_tanh_exp2", "silu", "silu_and_mul", "relu", "gemm_fp32",
            "gemm_f64", "linear_bias_gelu", "apply_epilogue", "split_k", "e4m3_decode",
            "e4m3_encode", "quantize_int8", "scaled_mm", "rel_to_max", "assert_close", "F"]
+
+
+# ------------------------------------------------------------------ MX (OCP microscaling) fp8
+
+
+def e8m0(s: torch.Tensor) -> torch.Tensor:
+    """E8M0 scale bytes as fp32: 2^(s - 127) (OCP MX v1.0 section 5.4; byte 255, NaN, unused)."""
+    return torch.pow(2.0, s.to(torch.float32) - 127.0)
+
+
+def mx_quant(x: torch.Tensor):
+    """Rows of x to fp8 e4m3 with an E8M0 scale a 32-column block, AITER's per_1x32 rule as the
+    reference states it (python/hk/mx.py:17-31): amax >= 2^-126, e = floor(log2 amax) - 8,
+    + 1 where amax > 448 * 2^e (so e = ceil(log2(amax / 448))); q = clamp(x / 2^e, +-448) cast
+    to e4m3 (nearest even); s = clamp(e + 127, 0, 254). Returns (q float8_e4m3fn, s uint8)."""
+    m, k = x.shape
+    v = x.float().reshape(m, k // 32, 32)
+    amax = v.abs().amax(-1).clamp_min(2.0 ** -126)
+    e = torch.floor(torch.log2(amax)) - 8
+    e = e + (amax > 448.0 * torch.pow(2.0, e)).float()
+    q = (v / torch.pow(2.0, e)[..., None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.reshape(m, k), (e + 127).clamp(0, 254).to(torch.uint8)
+
+
+def mx_dequant(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """fp8 rows q [M, K] with E8M0 scales s [M, K/32] -> fp32 (python/hk/mx.py:33-37)."""
+    return q.float() * e8m0(s).repeat_interleave(32, dim=-1)
+
+
+def mx_gemm(a: torch.Tensor, b: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor) -> torch.Tensor:
+    """(sa . A)(sb . B)^T in fp32 (the reference's check, tests/hk/gpu/test_mxfp8_gemm.py:27-31)."""
+    return mx_dequant(a, sa) @ mx_dequant(b, sb).t()

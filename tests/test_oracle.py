@@ -185,3 +185,71 @@ def test_rel_to_max_and_assert_close():
     assert O.rel_to_max(ref + torch.tensor([0.0, 0.04, 0.0]), ref) == pytest.approx(0.01)
     with pytest.raises(AssertionError):
         O.assert_close(ref * 1.1, ref, rtol=1e-2, atol=1e-2)
+
+
+# ------------------------------------------------------------------ MX fp8 (the oracle pinned)
+
+
+def test_e8m0_is_a_power_of_two():
+    s = torch.tensor([0, 100, 127, 130, 254], dtype=torch.uint8)
+    assert O.e8m0(s).tolist() == [2.0 ** -127, 2.0 ** -27, 1.0, 8.0, 2.0 ** 127]
+
+
+def test_mx_quant_hand_blocks():
+    """Blocks whose answer follows from the rule by hand: a max of exactly 448 keeps e = 0;
+    480 needs e = 1 (values halved); a max of 1 gives e = -8 (1 -> 256); a block of zeros
+    and a tiny block clamp their byte at 0 while q is scaled by the unclamped e."""
+    rows = [[448.0] + [1.0] * 31,
+            [480.0] + [0.5] * 31,
+            [1.0] + [0.25] * 31,
+            [0.0] * 32,
+            [2.0 ** -130] + [0.0] * 31]
+    x = torch.tensor(rows).to(torch.bfloat16)
+    q, s = O.mx_quant(x)
+    assert s.flatten().tolist() == [127, 128, 119, 0, 0]
+    qf = q.float()
+    assert qf[0, :2].tolist() == [448.0, 1.0]
+    assert qf[1, :2].tolist() == [240.0, 0.25]
+    assert qf[2, :2].tolist() == [256.0, 64.0]
+    assert (qf[3] == 0).all()
+    assert qf[4, 0].item() == 16.0  # 2^-130 / 2^-134
+
+
+def test_mx_quant_scale_is_the_smallest_that_fits():
+    """Every block of random rows (magnitudes 2^-20..2^20): the block max lands in (224, 448]
+    after scaling (one power of two less would overflow 448); dequant is within e4m3's half
+    ulp of x (relative 2^-4 at the block scale)."""
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(64, 256, generator=g) *
+         torch.exp2(torch.randint(-20, 20, (64, 1), generator=g).float())).to(torch.bfloat16)
+    q, s = O.mx_quant(x)
+    v = x.float().reshape(64, 8, 32)
+    scaled_max = v.abs().amax(-1) / O.e8m0(s)
+    assert (scaled_max <= 448.0).all() and (scaled_max > 224.0).all()
+    err = (O.mx_dequant(q, s) - x.float()).abs().reshape(64, 8, 32)
+    assert (err <= O.e8m0(s)[..., None] * 448.0 * 2.0 ** -4).all()
+
+
+def test_mx_quant_round_trips_representable_values():
+    """Values that are e4m3 numbers times the block's scale come back exactly."""
+    g = torch.Generator().manual_seed(8)
+    base = torch.randn(16, 128, generator=g).clamp(-440, 440).to(torch.float8_e4m3fn).float()
+    base[:, ::32] = 448.0  # pin every block's max, so e = 0 before the row factor
+    x = (base * torch.exp2(torch.randint(-6, 6, (16, 1), generator=g).float())).to(torch.bfloat16)
+    q, s = O.mx_quant(x)
+    assert torch.equal(O.mx_dequant(q, s), x.float())
+
+
+def test_mx_gemm_is_the_scaled_product():
+    """Against a float64 brute force over (m, n, k) with the scales applied term by term."""
+    g = torch.Generator().manual_seed(9)
+    m, n, k = 3, 5, 64
+    a = torch.randn(m, k, generator=g).to(torch.float8_e4m3fn)
+    b = torch.randn(n, k, generator=g).to(torch.float8_e4m3fn)
+    sa = torch.randint(120, 135, (m, k // 32), generator=g, dtype=torch.uint8)
+    sb = torch.randint(120, 135, (n, k // 32), generator=g, dtype=torch.uint8)
+    ref = [[sum(float(a[i, t]) * 2.0 ** (int(sa[i, t // 32]) - 127) *
+                float(b[j, t]) * 2.0 ** (int(sb[j, t // 32]) - 127) for t in range(k))
+            for j in range(n)] for i in range(m)]
+    got = O.mx_gemm(a, b, sa, sb).double()
+    assert torch.allclose(got, torch.tensor(ref, dtype=torch.float64), rtol=1e-5, atol=1e-6)
