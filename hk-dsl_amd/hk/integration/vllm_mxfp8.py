@@ -1,0 +1,151 @@
+"""vLLM's block-scaled MXFP8 linear layers on this build's MX GEMM (gfx950).
+
+Restates python/hk/integration/vllm_mxfp8.py (:1-225): vLLM serves 32 x 32 block-scaled
+MXFP8 checkpoints on gfx950 with `RocmDotScaledMxfp8LinearKernel`, whose `apply_weights`
+quantizes the activation (`mxfp8_e4m3_quantize`, AITER's per_1x32 rule) and calls
+`rocm_mxfp8_block32_gemm`. The patch wraps that class's two entry points:
+
+* `process_weights_after_loading` runs vLLM's, then lays the weight's 32 x 32 block scales
+  out one row each (`mxfp8.expand_block_scales`) beside vLLM's -- the OCP layout this build's
+  kernel reads;
+* `apply_weights` makes one call of the opaque op `hk_vllm::mxfp8_linear`. Inside it, where
+  M is a number, a call the route takes (`schedule`) quantizes the activation in one launch
+  (`mxfp8.quant`, the same bits as vLLM's quantizer) and runs `mxfp8.gemm`; every other
+  call runs vLLM's own quant and kernel.
+
+The route: N a multiple of 8 and K of 128 (the kernel's), and M >= MIN_M -- the reference's
+measured bound for its own kernel on the DeepSeek-V4.1 shapes (:35-36), used here until this
+build's kernel has a measured table of its own; `ENABLED = False` sends every call to vLLM.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Optional
+
+from . import engine
+
+_ORIG_PWAL: Optional[Callable] = None
+_ORIG_APPLY: Optional[Callable] = None
+
+#: The smallest M routed to hk.
+MIN_M = 2048
+#: Route hk-able calls to hk (True) or leave every call to vLLM (False).
+ENABLED = True
+
+
+def _fake(x, w, ws, hk_ws, out_dtype):
+    return x.new_empty((x.shape[0], w.shape[0]), dtype=out_dtype)
+
+
+PATCH = engine.Op("hk_vllm::mxfp8_linear",
+                  "mxfp8_linear(Tensor x, Tensor w, Tensor ws, Tensor hk_ws, ScalarType out_dtype)"
+                  " -> Tensor", _fake, paths=("hk", "fallback"), graph="safe")
+
+
+def schedule(m: int, n: int, k: int) -> bool:
+    """Whether hk takes an M x N x K call."""
+    return ENABLED and n % 8 == 0 and k % 128 == 0 and m >= MIN_M
+
+
+_VLLM: list = []
+
+
+def _vllm_path():
+    """(mxfp8_e4m3_quantize, rocm_mxfp8_block32_gemm): vLLM's own quant and kernel."""
+    if not _VLLM:
+        from vllm.model_executor.kernels.linear.mxfp8.rocm_block32_gemm import (  # noqa: PLC0415
+            rocm_mxfp8_block32_gemm)
+        from vllm.model_executor.layers.quantization.utils.mxfp8_utils import (  # noqa: PLC0415
+            mxfp8_e4m3_quantize)
+
+        _VLLM.extend((mxfp8_e4m3_quantize, rocm_mxfp8_block32_gemm))
+    return _VLLM
+
+
+def mxfp8_linear(x, w, ws, hk_ws, out_dtype):
+    """MXFP8-quantized bf16 x [M, K] @ w.T for a 32 x 32 block-scaled fp8 w [N, K]: this
+    build's quant and GEMM where the route takes the call, vLLM's otherwise."""
+    import torch  # noqa: PLC0415
+
+    from ..ops import mxfp8  # noqa: PLC0415
+
+    m, k = x.shape
+    n = w.shape[0]
+    if out_dtype == torch.bfloat16 and hk_ws.numel() and schedule(m, n, k):
+        PATCH.count("hk")
+        return mxfp8.linear(x, w, hk_ws)
+    PATCH.count("fallback")
+    quantize, gemm = _vllm_path()
+    xq, xs = quantize(x)
+    return gemm(xq, xs, w, ws, out_dtype)
+
+
+def process_weights_after_loading(self, layer) -> None:
+    """vLLM's, then the weight's block scales one row each, beside vLLM's."""
+    import torch  # noqa: PLC0415
+
+    from ..ops import mxfp8  # noqa: PLC0415
+
+    _ORIG_PWAL(self, layer)
+    w, ws = layer.weight, layer.weight_scale
+    n, k = w.shape
+    if ws.shape[0] == n or w.element_size() != 1 or n % 8 or k % 128:
+        return  # not the block-scaled path, or a shape the kernel does not take
+    rows = mxfp8.expand_block_scales(ws.data.view(torch.uint8))[:n]
+    layer.hk_ws = torch.nn.Parameter(rows, requires_grad=False)
+
+
+def apply_weights(self, layer, x, bias=None):
+    if not hasattr(layer, "hk_ws"):
+        return _ORIG_APPLY(self, layer, x, bias)
+    x2d = x.reshape(-1, x.shape[-1])
+    out = PATCH(x2d, layer.weight, layer.weight_scale, layer.hk_ws, x.dtype)
+    out = out.reshape(*x.shape[:-1], layer.weight.shape[0])
+    if bias is not None:
+        out = out + bias
+    return out
+
+
+def _cls():
+    from vllm.model_executor.kernels.linear.mxfp8 import rocm_native  # noqa: PLC0415
+
+    return rocm_native.RocmDotScaledMxfp8LinearKernel
+
+
+def apply_patch() -> str:
+    """Route vLLM's block-scaled MXFP8 linear layers. Returns what happened, in one line."""
+    global _ORIG_PWAL, _ORIG_APPLY
+    import importlib.util  # noqa: PLC0415
+
+    if importlib.util.find_spec("vllm") is None:
+        return "vllm is not importable; mxfp8 not patched"
+    if _ORIG_APPLY is not None:
+        return "mxfp8: already patched"
+    from ..target import current_arch  # noqa: PLC0415
+
+    if current_arch() != "gfx950":
+        return f"mxfp8: not patched -- gfx950's scaled MFMA, not {current_arch()}"
+    PATCH.define(mxfp8_linear)
+    cls = _cls()
+    _ORIG_PWAL, _ORIG_APPLY = cls.process_weights_after_loading, cls.apply_weights
+    cls.process_weights_after_loading = process_weights_after_loading
+    cls.apply_weights = apply_weights
+    return f"mxfp8 -> hk for block-scaled layers at M >= {MIN_M}"
+
+
+def revert() -> str:
+    global _ORIG_PWAL, _ORIG_APPLY
+    if _ORIG_APPLY is None:
+        return "mxfp8: not patched"
+    cls = _cls()
+    cls.process_weights_after_loading, cls.apply_weights = _ORIG_PWAL, _ORIG_APPLY
+    _ORIG_PWAL = _ORIG_APPLY = None
+    return "mxfp8 -> vllm"
+
+
+def status() -> str:
+    return "not patched" if _ORIG_APPLY is None else PATCH.summary()
+
+
+__all__ = ["PATCH", "schedule", "mxfp8_linear", "apply_patch", "revert", "status",
+           "process_weights_after_loading", "apply_weights"]

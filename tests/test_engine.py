@@ -155,3 +155,24 @@ def test_patch_contracts():
     p.count("a")
     assert p.stats == {"a": 2, "b": 0} and "a 2" in p.summary()
     assert p.guard(lambda v: v + 1)(1) == 2  # free outside capture
+
+
+def test_vllm_mxfp8_route_and_patch_without_vllm():
+    """The MXFP8 route takes whole shapes at M >= MIN_M only, and the patch reports, rather
+    than fails, where vLLM is absent (vllm_mxfp8.py:191-200's contract)."""
+    from hk.integration import vllm_mxfp8 as V
+
+    assert V.schedule(V.MIN_M, 5120, 4096)
+    assert not V.schedule(V.MIN_M - 1, 5120, 4096)
+    assert not V.schedule(4096, 5124, 4096)   # N % 8
+    assert not V.schedule(4096, 5120, 4000)   # K % 128
+    V.ENABLED = False
+    try:
+        assert not V.schedule(4096, 5120, 4096)
+    finally:
+        V.ENABLED = True
+    import importlib.util
+
+    if importlib.util.find_spec("vllm") is None:
+        assert "not importable" in V.apply_patch()
+    assert V.revert() == "mxfp8: not patched"

@@ -85,3 +85,21 @@ def test_mx_linear_is_quant_then_gemm():
     out = mxfp8.linear(x.to(DEV), w.to(DEV), ws.to(DEV))
     xq, xs = O.mx_quant(x)
     assert O.rel_to_max(out.cpu(), O.mx_gemm(xq, w, xs, ws)) < 5e-3
+
+
+def test_vllm_mxfp8_op_takes_the_hk_path():
+    """hk_vllm::mxfp8_linear's body at M >= MIN_M on a 32 x 32 block-scaled weight: this
+    build's quant and GEMM, right against the oracle (no vLLM needed on that path)."""
+    from hk.integration import vllm_mxfp8 as V
+
+    m, n, k = V.MIN_M, 512, 1024
+    x = _x(m, k, seed=11)
+    g = torch.Generator().manual_seed(12)
+    w = torch.randn(n, k, generator=g).to(torch.float8_e4m3fn)
+    blocks = torch.randint(120, 130, (n // 32, k // 32), generator=g, dtype=torch.uint8)
+    rows = mxfp8.expand_block_scales(blocks)
+    before = V.PATCH.stats["hk"]
+    out = V.mxfp8_linear(x.to(DEV), w.to(DEV), blocks.to(DEV), rows.to(DEV), torch.bfloat16)
+    assert V.PATCH.stats["hk"] == before + 1
+    xq, xs = O.mx_quant(x)
+    assert O.rel_to_max(out.cpu(), O.mx_gemm(xq, w, xs, rows)) < 5e-3
