@@ -214,7 +214,9 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
     if (sc == HKX_TILE_PINGPONG && !pp_ok)
       return fail(HKX_ERR_ARG, "the ping-pong tile kernel takes 256x256 tiles");
-    if (a->variant & ~(HKX_PP_MFMA32 | HKX_PP_ONE_TILE) || (a->variant && sc != HKX_TILE_PINGPONG))
+    if (sc == HKX_TILE_RING ? (a->variant & ~HKX_RING_WAVESPLIT) != 0
+                            : (a->variant & ~(HKX_PP_MFMA32 | HKX_PP_ONE_TILE)) != 0 ||
+                                  (a->variant && sc != HKX_TILE_PINGPONG))
       return fail(HKX_ERR_ARG, "variant %d", a->variant);
     p->schedule = sc;
     p->variant = a->variant;
@@ -302,6 +304,16 @@ int cu_count() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+// The columns of N whose 256 x 256 tiles fill whole waves of one-a-CU workgroups at M's
+// tile rows (0 where one wave takes more than N has): the reference's wave_cut
+// (python/hk/ops/gemm_cdna.py:923-930).
+int wave_cut(int m, int n, int outw) {
+  const int mb = (m + 255) / 256, cus = cu_count();
+  if (mb > cus) return 0;
+  const int per = cus / mb;
+  return (n / outw / per) * per * outw;
 }
 
 hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mode, dim3 grid,
@@ -419,8 +431,43 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       else if (ob == 1) mode = hkx::kStore8;
       else mode = hkx::kStoreF32;
     }
-    rc = launched(tile_dispatch(p, t, fp8, mode, grid, s), "tile GEMM");
-    if (rc) return rc;
+    const int cut = (p.variant & HKX_RING_WAVESPLIT) && !p.via_ws ? wave_cut(a.m, a.n, outw) : 0;
+    if (cut > 0 && cut < a.n) {
+      // whole waves of 256 x 256 tiles on the ring kernel, then the rest of N on 128 x 256
+      // tiles: B's rows, C's columns and the per-column epilogue operands from column cut
+      hkx::TileArgs t1 = t;
+      t1.N = cut;
+      t1.tiles_n = cut / outw;
+      rc = launched(tile_dispatch(p, t1, fp8, mode, dim3(t1.tiles_m * t1.tiles_n), s),
+                    "tile GEMM (whole waves)");
+      if (rc) return rc;
+      hkx::TileArgs t2 = t;
+      const int cb = elem_bytes(a.c_dtype);
+      t2.b = (const uint8_t*)a.b + (int64_t)cut * a.ldb * eb;
+      t2.b_bytes = (uint32_t)((p.pair ? 2LL * a.n - cut : (long long)a.n - cut) * a.ldb * eb);
+      t2.c = (uint8_t*)a.c + (int64_t)cut * cb;
+      t2.c_aligned = aligned(t2.c, 16) && (a.ldc * ob) % 16 == 0;
+      t2.N = a.n - cut;
+      t2.tiles_m = (a.m + 127) / 128;
+      t2.tiles_n = (t2.N + outw - 1) / outw;  // 128 x 256 tiles: the same output width
+      auto shift = [&](hkx::Opnd& o) {  // per-column vectors and tiles; broadcasts stay
+        if (o.p && ((o.kind == HKX_ROW && o.ld) || o.kind == HKX_TILE))
+          o.p = (const uint8_t*)o.p + (int64_t)cut * elem_bytes(o.dt);
+      };
+      shift(t2.ep.rs);
+      shift(t2.ep.ra);
+      shift(t2.ep.ta);
+      Plan p2 = p;
+      p2.schedule = HKX_TILE_W4;
+      p2.tile_m = 128;
+      p2.tile_n = 256;
+      rc = launched(tile_dispatch(p2, t2, fp8, mode, dim3(t2.tiles_m * t2.tiles_n), s),
+                    "tile GEMM (the rest of N)");
+      if (rc) return rc;
+    } else {
+      rc = launched(tile_dispatch(p, t, fp8, mode, grid, s), "tile GEMM");
+      if (rc) return rc;
+    }
   } else {
     hkx::DecodeArgs d{};
     d.a = a.a;

@@ -164,6 +164,12 @@ typedef struct HkxEpilogue {
 #define HKX_PP_MFMA32 1   /* 32 x 32 MFMA fragments (the fp8 and paired forms always use them) */
 #define HKX_PP_ONE_TILE 2 /* one tile a workgroup, instead of a grid of one workgroup a CU */
 
+/* HKX_TILE_RING variant bits. */
+#define HKX_RING_WAVESPLIT 4 /* the columns whose 256 x 256 tiles make whole waves of the CUs
+                                on the ring kernel, the rest of N on the 4-wave kernel's
+                                128 x 256 tiles (two launches; no split over K) -- the
+                                reference's ppw candidate (gemm_cdna.py:834-835, 923-930) */
+
 /* HKX_KERNEL_DECODE variant bits. */
 #define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K a multiple
                              of 1024 up to 32768, no split, unpaired); other calls take the

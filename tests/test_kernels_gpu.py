@@ -368,3 +368,52 @@ def test_decode_stream_fused_forms(m, nk):
                 cs=0, rs=1, ra=2, ta=3, act=nat.ACT_GELU_TANH, cmul=0.5, cadd=0.25)
     _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM, ep=ep)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("form", ["bias_gelu", "residual_colscale", "silu_mul", "fp8_deq_bias"])
+def test_ring_wave_split(form):
+    """HKX_RING_WAVESPLIT at 2048 rows (8 tile rows: 32 tile columns a wave of 256 CUs) and
+    N = 9216 (36 tile columns): columns 0-8191 on the ring kernel, 8192-9215 on 128 x 256
+    tiles, the per-column operands (bias, row scale) and the residual taken from column
+    8192 for the second launch; the paired form with its gate and up rows a full N apart."""
+    m, n, k = 2048, 9216, 512
+    g = torch.Generator().manual_seed(50)
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING,
+              variant=nat.RING_WAVESPLIT)
+    if form == "fp8_deq_bias":
+        a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
+        b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
+        sa = (torch.rand(m, 1, generator=g) + 0.5) / 448
+        sb = (torch.rand(n, generator=g) + 0.5) / 448
+        bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
+        _run(a8.to(DEV), b8.to(DEV), c, ep=_fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)],
+                                                  cs=0, rs=1, ra=2), **kw)
+        O.assert_close(c, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+        return
+    if form == "silu_mul":
+        a, b = _data(m, 2 * n, k, seed=51)
+        acc = O.gemm_fp32(a, b)
+        ref = O.silu_and_mul(acc[:, :n], acc[:, n:])
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        ep = nat.HkxEpilogue()
+        ep.form = nat.EP_SILU_MUL
+        _run(a.to(DEV), b.to(DEV), c, ep=ep, **kw)
+        O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+        return
+    a, b = _data(m, n, k, seed=52)
+    acc = O.gemm_fp32(a, b)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    if form == "bias_gelu":
+        bias = torch.randn(n, generator=g).to(torch.bfloat16)
+        ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
+        bd = bias.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
+    else:
+        res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+        rs = torch.rand(m, 1, generator=g) + 0.5
+        ref = acc * rs + res.float()
+        resd, rsd = res.to(DEV), rs.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(rsd, nat.COL), (resd, nat.TILE)], cs=0, ta=1), **kw)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
