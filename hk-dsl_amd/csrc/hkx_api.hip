@@ -59,7 +59,13 @@ struct Plan {
   bool pair;
   bool via_ws;    // fp32 shares / sum to ws, then the reduction
   size_t ws_bytes;
+  // HKX_RING_STREAMK: columns [0, sk_cut) in whole waves of ring tiles, the rest of N on
+  // ring tiles split sk_splits ways over K (sk_kper units each) into the workspace
+  int sk_cut, sk_splits, sk_kper;
 };
+
+int cu_count();
+int wave_cut(int m, int n, int outw);
 
 bool tile_shape_ok(int bm, int bn) {
   return (bm == 256 && bn == 256) || (bm == 128 && bn == 256) || (bm == 64 && bn == 256) ||
@@ -214,7 +220,8 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
     if (sc == HKX_TILE_PINGPONG && !pp_ok)
       return fail(HKX_ERR_ARG, "the ping-pong tile kernel takes 256x256 tiles");
-    if (sc == HKX_TILE_RING ? (a->variant & ~HKX_RING_WAVESPLIT) != 0
+    if (sc == HKX_TILE_RING ? (a->variant & ~(HKX_RING_WAVESPLIT | HKX_RING_STREAMK)) != 0 ||
+                                  (a->variant & HKX_RING_WAVESPLIT && a->variant & HKX_RING_STREAMK)
                             : (a->variant & ~(HKX_PP_MFMA32 | HKX_PP_ONE_TILE)) != 0 ||
                                   (a->variant && sc != HKX_TILE_PINGPONG))
       return fail(HKX_ERR_ARG, "variant %d", a->variant);
@@ -251,6 +258,28 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   p->via_ws = ws;
   const long long wcols = pair ? 2LL * a->n : a->n;
   p->ws_bytes = ws ? (size_t)p->splits * a->m * wcols * sizeof(float) : 0;
+  p->sk_cut = p->sk_splits = p->sk_kper = 0;
+  if (kernel == HKX_KERNEL_TILE && p->schedule == HKX_TILE_RING &&
+      (p->variant & HKX_RING_STREAMK) && !ws) {
+    // the rest of N past the whole waves, split over K so that its tiles fill the CUs
+    // (at least 4 K units a split, at most 8 splits)
+    const int outw = pair ? p->tile_n / 2 : p->tile_n;
+    const int cut = wave_cut(a->m, a->n, outw);
+    if (cut < a->n) {
+      const int rest = a->n - cut;
+      const int tiles = ((a->m + 255) / 256) * ((rest + outw - 1) / outw);
+      int sk = std::max(1, std::min({cu_count() / tiles, p->kunits / 4, 8}));
+      const int kper = (p->kunits + sk - 1) / sk;
+      sk = (p->kunits + kper - 1) / kper;
+      p->sk_cut = cut;
+      p->sk_splits = sk;
+      p->sk_kper = kper;
+      if (sk > 1) {
+        p->ws_bytes = (size_t)sk * a->m * (pair ? 2LL * rest : rest) * sizeof(float);
+        ws = true;
+      }
+    }
+  }
   if (ws && (!a->ws || a->ws_bytes < p->ws_bytes || !aligned(a->ws, 16)))
     return fail(HKX_ERR_WORKSPACE, "this plan needs a 16-byte aligned fp32 workspace of %zu bytes",
                 p->ws_bytes);
@@ -431,39 +460,78 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       else if (ob == 1) mode = hkx::kStore8;
       else mode = hkx::kStoreF32;
     }
-    const int cut = (p.variant & HKX_RING_WAVESPLIT) && !p.via_ws ? wave_cut(a.m, a.n, outw) : 0;
-    if (cut > 0 && cut < a.n) {
-      // whole waves of 256 x 256 tiles on the ring kernel, then the rest of N on 128 x 256
-      // tiles: B's rows, C's columns and the per-column epilogue operands from column cut
-      hkx::TileArgs t1 = t;
-      t1.N = cut;
-      t1.tiles_n = cut / outw;
-      rc = launched(tile_dispatch(p, t1, fp8, mode, dim3(t1.tiles_m * t1.tiles_n), s),
-                    "tile GEMM (whole waves)");
-      if (rc) return rc;
-      hkx::TileArgs t2 = t;
-      const int cb = elem_bytes(a.c_dtype);
-      t2.b = (const uint8_t*)a.b + (int64_t)cut * a.ldb * eb;
-      t2.b_bytes = (uint32_t)((p.pair ? 2LL * a.n - cut : (long long)a.n - cut) * a.ldb * eb);
-      t2.c = (uint8_t*)a.c + (int64_t)cut * cb;
-      t2.c_aligned = aligned(t2.c, 16) && (a.ldc * ob) % 16 == 0;
-      t2.N = a.n - cut;
-      t2.tiles_m = (a.m + 127) / 128;
-      t2.tiles_n = (t2.N + outw - 1) / outw;  // 128 x 256 tiles: the same output width
-      auto shift = [&](hkx::Opnd& o) {  // per-column vectors and tiles; broadcasts stay
-        if (o.p && ((o.kind == HKX_ROW && o.ld) || o.kind == HKX_TILE))
-          o.p = (const uint8_t*)o.p + (int64_t)cut * elem_bytes(o.dt);
-      };
-      shift(t2.ep.rs);
-      shift(t2.ep.ra);
-      shift(t2.ep.ta);
-      Plan p2 = p;
-      p2.schedule = HKX_TILE_W4;
-      p2.tile_m = 128;
-      p2.tile_n = 256;
-      rc = launched(tile_dispatch(p2, t2, fp8, mode, dim3(t2.tiles_m * t2.tiles_n), s),
-                    "tile GEMM (the rest of N)");
-      if (rc) return rc;
+    // The columns from c0 on as a call of their own: B's rows, C's columns and the
+    // per-column epilogue operands (vectors and tiles; broadcasts stay) from column c0.
+    auto from_col = [&](const hkx::TileArgs& t0, int c0) {
+      hkx::TileArgs r = t0;
+      r.b = (const uint8_t*)a.b + (int64_t)c0 * a.ldb * eb;
+      r.b_bytes = (uint32_t)((p.pair ? 2LL * a.n - c0 : (long long)a.n - c0) * a.ldb * eb);
+      r.c = (uint8_t*)a.c + (int64_t)c0 * elem_bytes(a.c_dtype);
+      r.c_aligned = aligned(r.c, 16) && (a.ldc * ob) % 16 == 0;
+      r.N = a.n - c0;
+      r.tiles_n = (r.N + outw - 1) / outw;
+      for (hkx::Opnd* o : {&r.ep.rs, &r.ep.ra, &r.ep.ta})
+        if (o->p && ((o->kind == HKX_ROW && o->ld) || o->kind == HKX_TILE))
+          o->p = (const uint8_t*)o->p + (int64_t)c0 * elem_bytes(o->dt);
+      return r;
+    };
+    const int cut = (p.variant & HKX_RING_WAVESPLIT) && !p.via_ws ? wave_cut(a.m, a.n, outw)
+                    : p.sk_cut;
+    if (cut < a.n && ((p.variant & HKX_RING_WAVESPLIT) ? cut > 0 : p.sk_splits > 0)) {
+      if (cut > 0) {  // whole waves of 256 x 256 tiles on the ring kernel
+        hkx::TileArgs t1 = t;
+        t1.N = cut;
+        t1.tiles_n = cut / outw;
+        rc = launched(tile_dispatch(p, t1, fp8, mode, dim3(t1.tiles_m * t1.tiles_n), s),
+                      "tile GEMM (whole waves)");
+        if (rc) return rc;
+      }
+      hkx::TileArgs t2 = from_col(t, cut);
+      if (p.variant & HKX_RING_WAVESPLIT) {  // the rest on 128 x 256 tiles
+        t2.tiles_m = (a.m + 127) / 128;
+        Plan p2 = p;
+        p2.schedule = HKX_TILE_W4;
+        p2.tile_m = 128;
+        p2.tile_n = 256;
+        rc = launched(tile_dispatch(p2, t2, fp8, mode, dim3(t2.tiles_m * t2.tiles_n), s),
+                      "tile GEMM (the rest of N)");
+        if (rc) return rc;
+      } else if (p.sk_splits == 1) {  // the rest on ring tiles, one pass
+        rc = launched(tile_dispatch(p, t2, fp8, mode, dim3(t2.tiles_m * t2.tiles_n), s),
+                      "tile GEMM (the rest of N)");
+        if (rc) return rc;
+      } else {  // the rest split over K: fp32 shares, then their sum and the epilogue
+        const long long wc2 = p.pair ? 2LL * t2.N : t2.N;
+        hkx::TileArgs t3 = t2;
+        t3.c = a.ws;
+        t3.ldc = wc2;
+        t3.split_stride = (int64_t)a.m * wc2;
+        t3.c_dt = HKX_FP32;
+        t3.ep = hkx::Fused{};
+        t3.ep.form = HKX_EP_NONE;
+        t3.kt_split = p.sk_kper;
+        Plan p3 = p;
+        p3.splits = p.sk_splits;
+        rc = launched(tile_dispatch(p3, t3, fp8, p.pair ? hkx::kPairWs : hkx::kStoreF32,
+                                    dim3(t3.tiles_m * t3.tiles_n, p.sk_splits), s),
+                      "tile GEMM (the rest of N, split over K)");
+        if (rc) return rc;
+        hkx::ReduceArgs r{};
+        r.ws = (const float*)a.ws;
+        r.split_stride = (int64_t)a.m * wc2;
+        r.ws_ld = wc2;
+        r.c = t2.c;
+        r.ldc = a.ldc;
+        r.splits = p.sk_splits;
+        r.M = a.m;
+        r.N = t2.N;
+        r.c_dt = a.c_dtype;
+        r.pair = p.pair;
+        r.f = t2.ep;
+        const dim3 rg(((t2.N + 3) / 4 + 255) / 256, a.m < 65535 ? a.m : 65535);
+        rc = launched(hkx::launch_reduce(r, a.ep, false, rg, s), "reduction (the rest of N)");
+        if (rc) return rc;
+      }
     } else {
       rc = launched(tile_dispatch(p, t, fp8, mode, grid, s), "tile GEMM");
       if (rc) return rc;

@@ -291,7 +291,7 @@ def gemm_candidates(m: int, n: int, k: int) -> List[str]:
     if 64 < m <= 2048:
         out += ["t128", "t128w8", "t128k2", "t128k4", "t256n128"]
     if m >= 256:
-        out += ["t256", "t256w", "t256k2", "t256w8"]
+        out += ["t256", "t256w", "t256sk", "t256k2", "t256w8"]
     return out
 
 

@@ -52,6 +52,9 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     # wave split: the columns whose 256 x 256 tiles fill whole waves of the CUs on the ring
     # kernel, the rest of N on 128 x 256 tiles (gemm_cdna.py:834-835's ppw)
     "t256w": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "variant": 4},
+    # stream-K: the whole waves likewise, the rest of N on 256 x 256 tiles split over K to
+    # fill the CUs (gemm_cdna.py:421-496's dp+sk mode; the shares summed by one pass)
+    "t256sk": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "variant": 8},
     "t128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 2},
     "t128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "w4", "splits": 4},
     "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},

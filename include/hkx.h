@@ -169,6 +169,12 @@ typedef struct HkxEpilogue {
                                 on the ring kernel, the rest of N on the 4-wave kernel's
                                 128 x 256 tiles (two launches; no split over K) -- the
                                 reference's ppw candidate (gemm_cdna.py:834-835, 923-930) */
+#define HKX_RING_STREAMK 8   /* the whole waves likewise on the ring kernel, the rest of N on
+                                ring tiles split over K so that they fill the CUs (fp32 shares
+                                in the workspace, then one pass that sums them in split order
+                                and applies the epilogue) -- the reference's dp+sk stream-K
+                                mode (gemm_cdna.py:421-496, 635-729) without its in-kernel
+                                fix-up; hkx_gemm_workspace() sizes the shares */
 
 /* HKX_KERNEL_DECODE variant bits. */
 #define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K a multiple

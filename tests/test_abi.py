@@ -123,6 +123,16 @@ def test_workspace_sizes():
     # a plan that needs a workspace refuses to run without one
     rc, msg = _check(_args(splits=2))
     assert rc == nat.ERR_WORKSPACE
+    # stream-K on the ring route: 2048 rows (8 tile rows, 32 tile columns a wave of the 256
+    # CUs this host-only call assumes), N = 9216: the last 1024 columns (32 tiles) split
+    # min(256 / 32, 8 K units / 4, 8) = 2 ways -> 2 shares of 2048 x 1024 fp32
+    sk = _args(m=2048, n=9216, k=512, tile_m=256, tile_n=256, tile_schedule=nat.TILE_RING,
+               variant=nat.RING_STREAMK)
+    assert L.hkx_gemm_workspace(ctypes.byref(sk)) == 2 * 2048 * 1024 * 4
+    sk.n = 8192  # whole waves: nothing is split
+    assert L.hkx_gemm_workspace(ctypes.byref(sk)) == 0
+    sk.variant = nat.RING_STREAMK | nat.RING_WAVESPLIT
+    assert _check(sk)[0] == nat.ERR_ARG
 
 
 def test_the_build_refuses_spills():

@@ -370,16 +370,19 @@ def test_decode_stream_fused_forms(m, nk):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("variant", [nat.RING_WAVESPLIT, nat.RING_STREAMK], ids=["ppw", "sk"])
 @pytest.mark.parametrize("form", ["bias_gelu", "residual_colscale", "silu_mul", "fp8_deq_bias"])
-def test_ring_wave_split(form):
+def test_ring_wave_split(form, variant):
     """HKX_RING_WAVESPLIT at 2048 rows (8 tile rows: 32 tile columns a wave of 256 CUs) and
     N = 9216 (36 tile columns): columns 0-8191 on the ring kernel, 8192-9215 on 128 x 256
     tiles, the per-column operands (bias, row scale) and the residual taken from column
-    8192 for the second launch; the paired form with its gate and up rows a full N apart."""
+    8192 for the second launch; the paired form with its gate and up rows a full N apart.
+    HKX_RING_STREAMK: the rest on 256 x 256 ring tiles split 2 ways over K into fp32
+    shares, summed with the epilogue by the reduction (one pass for fp8, whose 4 K units
+    make no split)."""
     m, n, k = 2048, 9216, 512
     g = torch.Generator().manual_seed(50)
-    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING,
-              variant=nat.RING_WAVESPLIT)
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, variant=variant)
     if form == "fp8_deq_bias":
         a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
         b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
