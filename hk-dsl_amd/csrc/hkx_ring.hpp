@@ -82,10 +82,11 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   constexpr int HS = 512 * 64;                 // one half-stage buffer
   constexpr int NBUF = 4;
   constexpr int EPO = NBUF * HS;  // epilogue operands: [tile parity][cs, rs, ra][256 slots]
-  constexpr int SCO = EPO + 2 * 3 * 1024;  // MX scales: [ring slot][512 rows] of 4 bytes
-  constexpr int SMEM = SCO + (MX ? NBUF * 2048 : 0);
+  // MX scales: [chunk % 3][512 rows] of 16 bytes, a chunk the E8M0 bytes of 8 half-stages
+  // (16 blocks of 32 K) of every A and B row of the tile
+  constexpr int SCO = EPO + 2 * 3 * 1024;
+  constexpr int SMEM = SCO + (MX ? 3 * 512 * 16 : 0);
   static_assert(!MX || FP8, "MX scales go with fp8 operands");
-  constexpr int NV = MX ? 5 : 4;  // vector-memory operations a wave's fill of a half-stage makes
   constexpr bool PAIR = (MODE == kPair16 || MODE == kPairWs);
   constexpr int OUTW = PAIR ? BN / 2 : BN;
   static_assert(!(PAIR && FP8) && !(MODE == kStore8 && PAIR), "modes");
@@ -147,6 +148,12 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   const __amdgpu_buffer_rsrc_t rsa = make_rsrc(MX ? p.sa : nullptr, MX ? p.sa_bytes : 0u);
   const __amdgpu_buffer_rsrc_t rsb = make_rsrc(MX ? p.sb : nullptr, MX ? p.sb_bytes : 0u);
   uint32_t fsa = 0, fsb = 0;  // this lane's scale row (MX)
+  // MX scale chunks a tile; chunks rotate through three LDS buffers across tiles too. A
+  // chunk's buffer is refilled three chunks later, three half-stages before that chunk's
+  // first read, so at least 2 + 2 - 3 half-stages after the old chunk's last one (every
+  // chunk is 2 half-stages or more): with two buffers a 2-half-stage chunk (the end of
+  // K = 1152) let the refill land under the other group's last reads.
+  const int cpt = (hpt + 7) >> 3;
   auto fill_tile = [&](int lt) {
     int m0, n0;
     tile_at(lt, m0, n0);
@@ -178,12 +185,18 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
       buf_load16_lds(i < 2 ? ra : rb, base + i * 8192, i < 2 ? fa : fb,
                      so + (uint32_t)(i & 1) * (i < 2 ? sa_step : sb_step));
     if constexpr (MX) {
-      // the E8M0 scales of this half-stage's 64 K (blocks 2 uk and 2 uk + 1 of 32): lane l
-      // of wave w takes the aligned dword that holds them for row 64 w + l (A rows, then B)
-      const uint32_t uk = (uint32_t)(2 * kt0 + f_kv);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wave < 4 ? rsa : rsb,
-          (__attribute__((address_space(3))) void*)(smem + SCO + (f_u & (NBUF - 1)) * 2048 + wave * 256),
-          4, wave < 4 ? fsa : fsb, __builtin_amdgcn_readfirstlane(4u * (uk >> 1)), 0, 0);
+      // every 8th half-stage of a tile, after its operands: the scales of the 8 from it on
+      // (16 bytes of E8M0 a row, blocks 2 uk .. 2 uk + 15), lane l of wave w for row
+      // 64 w + l (A rows, then B). Issued after the half-stage's own fills, it is done
+      // whenever they are, before that half-stage is read; one more load only makes the
+      // waits count stricter.
+      if ((f_kv & 7) == 0) {
+        const uint32_t uk = (uint32_t)(2 * kt0 + f_kv);
+        const int chunk = f_lt * cpt + (f_kv >> 3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wave < 4 ? rsa : rsb,
+            (__attribute__((address_space(3))) void*)(smem + SCO + (chunk % 3) * 8192 + wave * 1024),
+            16, wave < 4 ? fsa : fsb, __builtin_amdgcn_readfirstlane(2u * uk), 0, 0);
+      }
     }
     ++f_u;
     if (f_u < nu) {
@@ -250,23 +263,26 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   constexpr int FB = FR * 64;  // bytes of a fragment's rows in a buffer
   const int a_off = row0 * 64, b_off = (BM + col0) * 64;
   // MX: lanes l / 32 = h give the scale of 32-K block h of the MFMA's 64 for their fragment
-  // row: byte 2 (uk & 1) + h of the row's dword (uk: the half-stage's place in K, whose
-  // parity is u's), shifted down to byte 0, the MFMA's scale select
+  // row. Half-stage k of a tile (k % 8 = r in its chunk) has blocks 2 r and 2 r + 1 of the
+  // chunk: byte 2 (r & 1) + h of dword r / 2 of the row's 16 bytes, shifted down to byte 0,
+  // the MFMA's scale select.
   uint32_t sfa[FM], sfb[FN];
   const int sc_sh = 8 * (lane >> 5);
-  auto read_scales = [&](int u) {
+  auto read_scales = [&](int lt, int k) {
     if constexpr (MX) {
-      const uint32_t* sc = (const uint32_t*)(smem + SCO + (u & (NBUF - 1)) * 2048);
-      const int rf = lane & 31, sh = sc_sh + 16 * (u & 1);
+      const int r = k & 7;
+      const uint32_t* sc =
+          (const uint32_t*)(smem + SCO + ((lt * cpt + (k >> 3)) % 3) * 8192) + (r >> 1);
+      const int rf = lane & 31, sh = sc_sh + 16 * (r & 1);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) sfb[j] = sc[BM + col0 + 32 * j + rf] >> sh;
+      for (int j = 0; j < FN; ++j) sfb[j] = sc[4 * (BM + col0 + 32 * j + rf)] >> sh;
 #pragma unroll
-      for (int i = 0; i < FM; ++i) sfa[i] = sc[row0 + 32 * i + rf] >> sh;
+      for (int i = 0; i < FM; ++i) sfa[i] = sc[4 * (row0 + 32 * i + rf)] >> sh;
     }
   };
-  auto read_frags = [&](int u, Frag (&af)[FM], Frag (&bf)[FN]) {
+  auto read_frags = [&](int u, int lt, int k, Frag (&af)[FM], Frag (&bf)[FN]) {
     const uint8_t* s = smem + (u & (NBUF - 1)) * HS;
-    read_scales(u);
+    read_scales(lt, k);
     if constexpr (FP8) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -463,17 +479,17 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   fill_next();
   fill_next();
   fill_next();
-  __builtin_amdgcn_s_waitcnt(wait_vm(2 * NV));  // this wave's share of half-stage 0 landed
+  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // this wave's share of half-stage 0 landed
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();
   int u = 0;
   for (int lt = 0; lt < my_tiles; ++lt) {
     for (int k = 0; k < hpt; ++k, ++u) {
       // memory phase
-      read_frags(u, af, bf);
+      read_frags(u, lt, k, af, bf);
       if (k == 0 && lt + 1 < my_tiles) ep_load(lt + 1);
       fill_next();
-      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * NV));
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -483,7 +499,7 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
       else mma(af, bf, std::false_type{});
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(wait_vm(2 * NV));
+      __builtin_amdgcn_s_waitcnt(wait_vm(8));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     }

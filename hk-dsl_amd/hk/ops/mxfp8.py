@@ -5,8 +5,9 @@ K-contiguous (F.linear's layout); sa (M, K/32) and sb (N, K/32) their E8M0 scale
 a row and 32 columns (the OCP MX layout; a 32 x 32-block weight scale is its rows repeated,
 `expand_block_scales`). Here the product runs on the ring GEMM kernel's MX form: every MFMA
 is gfx950's scaled one (v_mfma_scale_f32_32x32x64_f8f6f4), each lane passing the E8M0 byte
-of its own fragment row and 32-K block; the scales reach LDS with the half-stage they
-belong to, by the same DMA as the operands. K a multiple of 128, N of 8, any M.
+of its own fragment row and 32-K block; the scales reach LDS by the same DMA as the
+operands, 16 bytes a row every 8 half-stages (whole lines: one 4-byte load a row and
+half-stage doubled the L2 requests and cost 60%). K a multiple of 128, N of 8, any M.
 
 `quant(x)` is the activation side (python/hk/ops/mxfp8.py:605-660): bf16 x to fp8 e4m3 and
 E8M0 scales by AITER's per_1x32 rule (python/hk/mx.py:17-31), in one launch, the scales in

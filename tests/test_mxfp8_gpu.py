@@ -29,8 +29,12 @@ def _operands(m, n, k, seed, block_weight_scales=False):
 
 @pytest.mark.parametrize("m,n,k,blk", [(256, 256, 512, True), (512, 384, 1280, True),
                                        (300, 512, 1152, False), (1, 256, 128, False),
-                                       (2100, 2048, 2048, False)])
+                                       (2100, 2048, 2048, False), (4096, 4352, 128, False),
+                                       (4096, 4352, 1152, True)])
 def test_mx_gemm_matches_the_scaled_product(m, n, k, blk):
+    """Whole and partial chunks of 8 half-stages of scales (K = 1152: 18 half-stages, its last
+    chunk two), the shortest K (128: a two-half-stage chunk a tile, two tiles a workgroup at
+    4096 x 4352), ragged M."""
     a, b, sa, sb = _operands(m, n, k, seed=m + n + k, block_weight_scales=blk)
     print(f"case mx_gemm {m}x{n}x{k}", flush=True)
     out = mxfp8.gemm(a.to(DEV), b.to(DEV), sa.to(DEV), sb.to(DEV))
