@@ -1,25 +1,22 @@
-// The persistent 256 x 256 MFMA GEMM for gfx950: 4 waves (2 x 2), each a 128 x 128 block
-// of C -- 256 fp32 accumulators a lane in AGPRs, one wave a SIMD. One workgroup a CU walks
-// its tiles (every gridDim.x-th) with one continuous LDS pipeline across tile boundaries.
+// The persistent 256 x 256 MFMA GEMM for gfx950: 8 waves in two groups of four (one wave of
+// each group a SIMD), each wave a 64 x 128 block of C (128 fp32 accumulators a lane). One
+// workgroup a CU walks its tiles (every gridDim.x-th, XCD-aware numbering, grouped raster)
+// with one continuous LDS pipeline across tile boundaries.
 //
-// Why this shape and this pipeline:
-// * LDS traffic. A K stage costs each wave (its A rows + its B rows) x the stage width in
-//   fragment reads; four 128 x 128 wave blocks read 128 KB a 128-byte stage, where eight
-//   64 x 128 blocks read 192 KB. Under the power limit the chip reaches on dense bf16 MFMA
-//   work, every byte moved through the LDS is clock taken from the matrix cores.
+// Why this schedule:
+// * Ping-pong. The groups are one phase apart: while one issues a half-stage's MFMAs at raised
+//   priority, the other reads the next half-stage's fragments from LDS and issues fills; a
+//   barrier of all 8 waves ends every phase. A single wave's ds_read_b128 stream runs at a
+//   quarter of the LDS's rate on gfx950, so one wave a SIMD cannot both feed a 128 x 128
+//   block and keep its MFMAs busy; two waves taking turns can.
 // * Fill latency. K advances in half-stages (64 bytes of every row) through a ring of four
-//   32 KB buffers. Half-stage u + 4 is filled into u's buffer as soon as every wave is past
-//   u's last fragment read, and must have landed one half-stage before it is read: three
-//   half-stages (~3000 MFMA cycles) to hide the L2 / MALL / HBM latency, where a
-//   double-buffered 128-byte stage leaves about one.
-// * MFMA: bf16 as v_mfma_f32_16x16x32_bf16 (8 x 8 fragments of 16 x 16 a wave; one k-step
-//   is a whole half-stage), fp8 e4m3 as v_mfma_scale_f32_32x32x64_f8f6f4 (4 x 4 fragments
-//   of 32 x 32, one k-step a half-stage). B's fragment is the first operand, so a lane ends
-//   with runs of four consecutive columns of one row of C.
-// * One barrier a half-stage, before its MFMAs: it is the read-after-fill edge for
-//   half-stage u + 1, whose fragments are read under u's MFMAs (each wave waits for its own
-//   fills of u + 1 -- vmcnt -- and its reads of u -- lgkmcnt -- first), and the
-//   fill-after-read edge for u's buffer, refilled with u + 4 right after it.
+//   32 KB buffers. Half-stage u + 3 is filled into the buffer u - 1 used, once every wave is
+//   past u - 1's reads: three half-stages (~6 phases) to hide the L2 / MALL / HBM latency.
+// * MFMA: bf16 as v_mfma_f32_16x16x32_bf16 (4 x 8 fragments of 16 x 16 a wave; one k-step is
+//   a half-stage), fp8 e4m3 as v_mfma_scale_f32_32x32x64_f8f6f4 (2 x 4 fragments of 32 x 32).
+//   B's fragment is the first operand, so a lane ends with runs of four consecutive columns
+//   of one row of C. The MX form passes each lane's E8M0 byte for its fragment row and 32-K
+//   block as the MFMA's scales.
 // * Tile boundaries cost nothing in the pipeline: the fills of the next tile's first
 //   half-stages are in flight while this tile's last k-steps run and its epilogue is
 //   applied; the epilogue goes from the accumulators straight to global memory (no LDS
@@ -32,15 +29,15 @@
 //   the same DMA as the fills, double-buffered by tile parity, at the tile's start; a TILE
 //   operand (residual) is read from global memory in the epilogue.
 //
-// Fills: wave w's instruction i moves rows 64 i + 16 w + [0, 16) of a half-stage (A rows
-// 0-255, B rows 256-511); lane l writes bytes 16 l of that 1 KB (row + l / 4, physical
+// Fills: wave w's instruction i moves rows 128 i + 16 w + [0, 16) of a half-stage's A
+// (i < 2) or B (i >= 2) rows; lane l writes bytes 16 l of that 1 KB (row + l / 4, physical
 // chunk l % 4). A row's four 16-byte chunks are stored XOR-swizzled by bits 3 and 4 of the
 // row (chunk c at c ^ swz4(r)), so the fragment reads -- 16 rows of four chunks, or 32 rows
 // of one -- are conflict-free; the swizzle is applied on the global side.
 //
 // Ragged M and N edges read zeros through the buffer resources' bounds; stores are
 // predicated on n < N and dropped past M by the store's buffer bounds (the host sends
-// N % 8 != 0 or an unaligned C elsewhere).
+// N % 8 != 0, an unaligned C or a C of 4 GiB or more elsewhere).
 #pragma once
 
 #include "hkx_tile.hpp"
