@@ -29,7 +29,7 @@
 //   the same DMA as the fills, double-buffered by tile parity, at the tile's start; a TILE
 //   operand (residual) is read from global memory in the epilogue.
 //
-// Fills: wave w's instruction i moves rows 128 i + 16 w + [0, 16) of a half-stage's A
+// Fills: wave w's instruction i moves rows 128 (i % 2) + 16 w + [0, 16) of a half-stage's A
 // (i < 2) or B (i >= 2) rows; lane l writes bytes 16 l of that 1 KB (row + l / 4, physical
 // chunk l % 4). A row's four 16-byte chunks are stored XOR-swizzled by bits 3 and 4 of the
 // row (chunk c at c ^ swz4(r)), so the fragment reads -- 16 rows of four chunks, or 32 rows
