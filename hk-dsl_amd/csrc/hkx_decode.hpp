@@ -176,8 +176,10 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 //   row (piece c at c ^ (r % 16)), applied on the global side, so the MFMA fragment reads
 //   (16 rows, one piece each) are conflict-free.
 // * X is the same for every block: wave w owns the 128-element group w of every chunk, and
-//   loads its share of X (CPB groups of 16 rows) into registers once; past K = 4096 it is
-//   streamed with the chunks instead (two chunks ahead, three register slots).
+//   loads its share of X (CPB groups of 16 rows) into registers once, a chunk's share with
+//   the first block's fill of the chunk before it (all of X up front cost 1 us of
+//   20 at M = 16, K = 4096); past K = 4096 it is streamed with the chunks instead (two
+//   chunks ahead, three register slots).
 // * v_mfma_f32_16x16x32_bf16 with W's fragment first; the 8 waves' partial sums of a block
 //   meet in LDS (double-buffered by block parity), and wave 0 sums, applies the epilogue and
 //   stores after the next chunk's barrier, under the other waves' MFMAs.
@@ -316,12 +318,20 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
   };
 
-  // chunk q landed (all but this wave's newest loads: those of chunks q + 1 and q + 2,
-  // fewer at the end) and every wave is done with chunk q - 1, whose slot the fill of
-  // q + 3 takes; lgkmcnt(0) as well
+  // X for chunk k (its group of this wave) goes to registers by loads issued just before
+  // the fill of chunk k + 1: x0 f0 x1 f1 f2, then step q issues x(q + 2) and f(q + 3). X for
+  // a chunk exists for every chunk with CPB = 0 (streamed), for the first CPB with CPB > 0
+  // (held across the walk).
+  auto has_x = [&](int k) { return k < nq && (CPB == 0 || k < CPB); };
+  // chunk q and its X landed, and every wave is done with chunk q - 1, whose slot the fill
+  // of q + 3 takes: in issue order the loads after x(q) and f(q) are f(q + 1), x(q + 1) and
+  // f(q + 2), each 4 a wave where it exists (anything issued later only makes the wait
+  // stricter); lgkmcnt(0) as well
   auto wait_chunk = [&](int q) {
-    if (q + 2 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
-    else if (q + 1 < nq) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
+    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq) + has_x(q + 1));
+    if (n >= 12) __builtin_amdgcn_s_waitcnt(wait_vm_dec(12) & ~(15 << 8));
+    else if (n == 8) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
+    else if (n == 4) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
     else __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
   };
   auto block_done = [&](int j) {
@@ -337,18 +347,15 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   };
 
   if constexpr (CPB > 0) {
-    // X held in registers for the whole walk, loaded first; then chunks 0-2 in flight.
-    // Waiting for all but the 12 newest loads leaves the chunks in flight and X landed
-    // (with fewer than 3 chunks the first wait of the loop, which counts what was issued,
-    // sees to X).
+    // X held in registers for the whole walk, its chunks loaded with the first block's
+    // fills, so a workgroup starts on 32 KB of X rather than all of it
     i32x4 x[CPB][4];
-#pragma unroll
-    for (int c = 0; c < CPB; ++c) xload(c, x[c]);
     ep_load(0);
+    xload(0, x[0]);
     fill(0);
+    if (CPB > 1) xload(1, x[CPB > 1 ? 1 : 0]);
     fill(1);
     fill(2);
-    __builtin_amdgcn_s_waitcnt(wait_vm_dec(12));
     for (int j = 0; j < my_blocks; ++j) {
 #pragma unroll
       for (int c = 0; c < CPB; ++c) {
@@ -356,6 +363,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
         wait_chunk(q);
         __builtin_amdgcn_s_barrier();
         if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);  // older than the fills of q + 3 on
+        if (c + 2 < CPB && j == 0) xload(c + 2, x[c + 2 < CPB ? c + 2 : 0]);
         fill(q + 3);
         if (c == 0 && j > 0 && wave == 0) finish(j - 1);
         mma(q, x[c]);
@@ -363,27 +371,25 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       block_done(j);
     }
   } else {
-    // K past 4096: X streamed with the chunks, two ahead, through three register slots
-    // (the loop is unrolled by three so every slot is a fixed register set). A chunk's X
-    // loads follow the fill of the chunk three ahead, so the loads issued after chunk q's
-    // are again those of chunks q + 1 and q + 2, and the same waits hold.
+    // K past 4096: X streamed with the chunks through three register slots (the loop is
+    // unrolled by three so every slot is a fixed register set)
     i32x4 xs[3][4];
     auto xnext = [&](int q, i32x4 (&dst)[4]) {
-      if (q < nq) xload(q % cpb, dst);
+      if (has_x(q)) xload(q % cpb, dst);
     };
     ep_load(0);
-    fill(0);
-    fill(1);
     xnext(0, xs[0]);
-    fill(2);
+    fill(0);
     xnext(1, xs[1]);
+    fill(1);
+    fill(2);
     auto step = [&](int q, const i32x4 (&xc)[4], i32x4 (&xn)[4]) {
       const int j = q / cpb, c = q - j * cpb;
       wait_chunk(q);
       __builtin_amdgcn_s_barrier();
       if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);
-      fill(q + 3);
       xnext(q + 2, xn);
+      fill(q + 3);
       if (c == 0 && j > 0 && wave == 0) finish(j - 1);
       mma(q, xc);
       if (c == cpb - 1) block_done(j);

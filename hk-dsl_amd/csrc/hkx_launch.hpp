@@ -46,7 +46,8 @@ hipError_t launch_mx_quant(const void* x, int64_t ldx, void* q, int64_t ldq, uin
 hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mode, dim3 grid,
                          hipStream_t s);
 
-// The streaming decode kernel (stream_kernel): M <= 16, K <= 4096, no split, unpaired.
+// The streaming decode kernel (stream_kernel): M <= 16, K a multiple of 1024 up to 32768,
+// no split, unpaired.
 bool stream_takes(const DecodeArgs& a, int splits, bool pair);
 hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s);
 
