@@ -5,7 +5,7 @@
 //
 // The epilogue semantics follow hk.templates.gemm (python/hk/templates/gemm.py):
 // operands are loaded in their layout and converted to fp32 (:212-226), the
-// tanh-GELU is the exp2/rsqrt form of :814-837, silu is x * sigmoid(x) (:845-847).
+// tanh-GELU is the exp2 form of :814-837 (a reciprocal where it squares a rsqrt), silu is x * sigmoid(x) (:845-847).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,6 +17,7 @@
 
 namespace hkx {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -74,16 +75,15 @@ HKX_DEV f32x4 unpack_f16x4(u32x2 w) {
 }
 
 // Round to nearest even (the hardware's conversion on gfx950: v_cvt_pk_bf16_f32).
+// two floats to a packed pair, round to nearest even (one v_cvt_pk_* for the pair)
 HKX_DEV uint32_t pack_bf16x2(float a, float b) {
-  uint16_t lo = __builtin_bit_cast(uint16_t, (__bf16)a);
-  uint16_t hi = __builtin_bit_cast(uint16_t, (__bf16)b);
-  return (uint32_t)lo | ((uint32_t)hi << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2_t));
 }
 
 HKX_DEV uint32_t pack_f16x2(float a, float b) {
-  uint16_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
-  uint16_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
-  return (uint32_t)lo | ((uint32_t)hi << 16);
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2_t));
 }
 
 // fp32 -> OCP e4m3 (float8_e4m3fn), round to nearest even, saturating at +-448
@@ -156,8 +156,9 @@ HKX_DEV f32x4 ld_tile(const Opnd& o, int m, int n) {
 // ---------------------------------------------------------------- pointwise math
 
 // tanh-GELU as x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3):
-// sigmoid(2u) = 1 / (1 + 2^(x (A x^2 + B))), and since that denominator is >= 1,
-// 1/d = rsqrt(d)^2 -- one v_exp_f32 and one v_rsq_f32 (templates/gemm.py:814-837).
+// sigmoid(2u) = 1 / (1 + 2^(x (A x^2 + B))) -- one v_exp_f32 and one v_rcp_f32 (the
+// reference squares a v_rsq_f32 instead, templates/gemm.py:814-837: one more multiply).
+// At x -> -inf the power is +inf and its reciprocal 0, so the product stays finite.
 constexpr float kGeluB = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
 constexpr float kGeluA = kGeluB * 0.044715f;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -168,9 +169,7 @@ HKX_DEV float gelu_tanh(float x) {
   q = __builtin_fmaf(q, kGeluA, kGeluB);
   q *= x;
   q = __builtin_amdgcn_exp2f(q);
-  q += 1.0f;
-  q = __builtin_amdgcn_rsqf(q);
-  return x * q * q;
+  return x * __builtin_amdgcn_rcpf(1.0f + q);
 }
 
 // silu(x) = x * sigmoid(x) = x / (1 + e^-x); at x -> -inf, e^-x -> inf and the

@@ -432,6 +432,12 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
       // gate/up pairs) trade quarters: after the swap quarter q holds columns
       // 8 (q / 2) + [0, 8) of fragment a (q even) or b (q odd).
       const int q = h;
+      // a bias is the same for the FM row fragments: read and widened once a column
+      [[maybe_unused]] f32x4 bias_v[FN];
+      if constexpr (EPF == kEpBias && !PAIR) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bias_v[j] = slot4(eo + 512 + col0 + 16 * j + 4 * q, HKX_BF16);
+      }
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int ml = row0 + 16 * i + rf;
@@ -445,6 +451,10 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
             va = silu_mul4(run(i, j, 0), run(i, j + 1, 0));
             vb = silu_mul4(run(i, j + 2, 0), run(i, j + 3, 0));
             ca = ((wn * FN + j) >> 1) * 16;
+          } else if constexpr (EPF == kEpBias) {
+            ca = col0 + 16 * j;
+            va = act4c<ACT>(0, run(i, j, 0) + bias_v[j]);
+            vb = act4c<ACT>(0, run(i, j + 1, 0) + bias_v[j + 1]);
           } else {
             ca = col0 + 16 * j;
             va = apply(run(i, j, 0), ml, ca + 4 * q, cs);
