@@ -595,9 +595,29 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
   return HKX_OK;
 }
 
+// The MX GEMM's K split: where its 256 x 256 tiles fill less than half the CUs, up to 8
+// splits of at least 8 k-tiles (1024 K) each, so the tiles times the splits stay within
+// the CUs; none where an fp32 share would span 4 GiB. (Shorter splits lost more to the
+// shares' round trip than they gained: K = 1152 and 1280 ran slower split in two.)
+static int mx_splits(int32_t m, int32_t n, int32_t k) {
+  if (m < 1 || n < 1 || k < 128 || k % 128) return 1;
+  const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  const int cu = cu_count();
+  if (2 * tiles > cu || (long long)m * n * 4 >= (1LL << 32)) return 1;
+  const int s = std::min(std::min(cu / tiles, (k / 128) / 8), 8);
+  if (s < 2) return 1;
+  const int kper = (k / 128 + s - 1) / s;  // no empty last split
+  return (k / 128 + kper - 1) / kper;
+}
+
+size_t hkx_mx_gemm_workspace(int32_t m, int32_t n, int32_t k) {
+  const int s = mx_splits(m, n, k);
+  return s > 1 ? (size_t)s * (size_t)m * (size_t)n * 4u : 0;
+}
+
 int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const uint8_t* sa,
                 int64_t sa_ld, const uint8_t* sb, int64_t sb_ld, void* c, int64_t ldc, int32_t m,
-                int32_t n, int32_t k, void* stream) {
+                int32_t n, int32_t k, void* ws, size_t ws_bytes, void* stream) {
   g_err.clear();
   if (!a || !b || !c || !sa || !sb) return fail(HKX_ERR_ARG, "mx_gemm: a null pointer");
   if (m < 1 || n < 1 || k < 1) return fail(HKX_ERR_SHAPE, "mx_gemm: M=%d N=%d K=%d", m, n, k);
@@ -640,8 +660,42 @@ int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const ui
   t.sb_ld = (uint32_t)sb_ld;
   t.sa_bytes = (uint32_t)((long long)m * sa_ld);
   t.sb_bytes = (uint32_t)((long long)n * sb_ld);
-  const dim3 g(std::min(t.tiles_m * t.tiles_n, cu_count()));
-  return launched(hkx::launch_ring_mx(t, g, (hipStream_t)stream), "mx GEMM");
+  const int splits = mx_splits(m, n, k);
+  const hipStream_t s = (hipStream_t)stream;
+  if (splits == 1) {
+    const dim3 g(std::min(t.tiles_m * t.tiles_n, cu_count()));
+    return launched(hkx::launch_ring_mx(t, false, g, s), "mx GEMM");
+  }
+  const size_t need = hkx_mx_gemm_workspace(m, n, k);
+  if (!ws || ws_bytes < need || !aligned(ws, 16))
+    return fail(HKX_ERR_WORKSPACE, "mx_gemm: needs %zu bytes of 16-byte aligned workspace, got %zu",
+                need, ws ? ws_bytes : (size_t)0);
+  // split s of K into fp32 share s (M x N, row stride N), one tile a workgroup
+  hkx::TileArgs tw = t;
+  tw.c = ws;
+  tw.ldc = n;
+  tw.split_stride = (int64_t)m * n;
+  tw.c_dt = HKX_FP32;
+  tw.kt_split = (k / 128 + splits - 1) / splits;
+  int rc = launched(hkx::launch_ring_mx(tw, true, dim3(t.tiles_m * t.tiles_n, splits), s),
+                    "mx GEMM (split over K)");
+  if (rc) return rc;
+  hkx::ReduceArgs r{};
+  r.ws = (const float*)ws;
+  r.split_stride = (int64_t)m * n;
+  r.ws_ld = n;
+  r.c = c;
+  r.ldc = ldc;
+  r.splits = splits;
+  r.M = m;
+  r.N = n;
+  r.c_dt = HKX_BF16;
+  r.pair = 0;
+  r.f = t.ep;
+  HkxEpilogue none{};
+  none.form = HKX_EP_NONE;
+  const dim3 rg(((n + 3) / 4 + 255) / 256, m < 65535 ? m : 65535);
+  return launched(hkx::launch_reduce(r, none, false, rg, s), "mx GEMM (sum of the splits)");
 }
 
 int hkx_mx_quant(const void* x, int64_t ldx, void* q, int64_t ldq, uint8_t* s, int64_t lds,

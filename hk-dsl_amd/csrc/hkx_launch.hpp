@@ -37,8 +37,9 @@ bool ring_takes(const TileArgs& a, bool fp8, int mode);
 hipError_t launch_ring(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
 hipError_t launch_ring_bf16(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
 hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
-// The MX form (fp8 operands, E8M0 block scales in a.sa / a.sb): bf16 C, no epilogue.
-hipError_t launch_ring_mx(const TileArgs& a, dim3 grid, hipStream_t s);
+// The MX form (fp8 operands, E8M0 block scales in a.sa / a.sb), no epilogue: bf16 C, or
+// fp32 shares of a K split (f32_shares, a.c the workspace, grid.y the splits).
+hipError_t launch_ring_mx(const TileArgs& a, bool f32_shares, dim3 grid, hipStream_t s);
 // MX quantization of bf16 rows (hkx_mx_quant).
 hipError_t launch_mx_quant(const void* x, int64_t ldx, void* q, int64_t ldq, uint8_t* sc,
                            int64_t lds, int m, int k, hipStream_t s);

@@ -23,9 +23,13 @@ hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 g
   return hipGetLastError();
 }
 
-hipError_t launch_ring_mx(const TileArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((ring_kernel<true, kStore16, HKX_ACT_NONE, kEpNone, true>), grid, dim3(512), 0,
-                     s, a);
+hipError_t launch_ring_mx(const TileArgs& a, bool f32_shares, dim3 grid, hipStream_t s) {
+  if (f32_shares)
+    hipLaunchKernelGGL((ring_kernel<true, kStoreF32, HKX_ACT_NONE, kEpNone, true>), grid,
+                       dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((ring_kernel<true, kStore16, HKX_ACT_NONE, kEpNone, true>), grid,
+                       dim3(512), 0, s, a);
   return hipGetLastError();
 }
 

@@ -73,7 +73,8 @@ class HkxGemmArgs(Structure):
 
 #: Every function include/hkx.h declares.
 SYMBOLS = ("hkx_abi_version", "hkx_abi_sizes", "hkx_last_error", "hkx_gemm_workspace",
-           "hkx_gemm_check", "hkx_gemm", "hkx_scaled_mm", "hkx_mx_gemm", "hkx_mx_quant")
+           "hkx_gemm_check", "hkx_gemm", "hkx_scaled_mm", "hkx_mx_gemm", "hkx_mx_gemm_workspace",
+           "hkx_mx_quant")
 
 _LIB = None
 _LOCK = threading.Lock()
@@ -114,7 +115,9 @@ def lib() -> ctypes.CDLL:
         L.hkx_gemm.argtypes = [POINTER(HkxGemmArgs), c_void_p]
         L.hkx_mx_gemm.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32,
-                                  c_int32, c_void_p]
+                                  c_int32, c_void_p, c_size_t, c_void_p]
+        L.hkx_mx_gemm_workspace.argtypes = [c_int32, c_int32, c_int32]
+        L.hkx_mx_gemm_workspace.restype = c_size_t
         L.hkx_mx_quant.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                    c_int32, c_int32, c_void_p]
         L.hkx_scaled_mm.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,

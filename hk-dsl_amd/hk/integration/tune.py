@@ -25,8 +25,15 @@ and its replays timed with events, the paths interleaved over `rounds` rounds; a
 time is its median round. Launch overhead is inside the graph for every path alike. Each
 path's output is checked against fp32 first; a path that misses the tolerance is not timed.
 
+A third, ``routes_vllm_mxfp8_gfx950.json`` (read by `vllm_mxfp8.schedule`), has the same
+form for vLLM's block-scaled MXFP8 linears: per (N, K) of `MX_SHAPES`, hk's route (its
+activation quant, then `mxfp8.gemm`) against the engine's, timed with the same
+quant; the engine here is hipBLASLt's MX GEMM (`torch._scaled_mm` with E8M0 block scales),
+since vLLM's own kernel (AITER's) is not importable on this machine.
+
     python -m hk.integration.tune gemm --out hk/tuned/routes_gemm_gfx950.json
     python -m hk.integration.tune vllm_linear --out hk/tuned/routes_vllm_linear_gfx950.json
+    python -m hk.integration.tune vllm_mxfp8 --out hk/tuned/routes_vllm_mxfp8_gfx950.json
 """
 
 from __future__ import annotations
@@ -55,6 +62,17 @@ GEMM_MS = (1, 4, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192)
 MAX_SEQS = 256
 #: fp32-relative tolerance a path must meet before it is timed.
 CHECK_TOL = 2e-2
+
+#: (N, K) of the block-scaled MXFP8 linears the reference measured its route on
+#: (python/hk/integration/vllm_mxfp8.py:33-36: DeepSeek-V4.1-Flash's prefill projections
+#: at TP2, and the indexer's wq_b).
+MX_SHAPES: Dict[Tuple[int, int], str] = {
+    (1792, 5120): "dsv4_proj", (2304, 5120): "dsv4_proj", (5120, 1152): "dsv4_proj",
+    (5120, 4096): "dsv4_proj", (16384, 1280): "dsv4_proj", (12800, 6144): "engram_wkv",
+    (4096, 1280): "indexer_wq_b"}
+#: The Ms of the MXFP8 table: from decode batches to long prefills.
+MX_GRID = (16, 32, 64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192,
+           16384)
 
 #: The config.json fields the shapes need, of the models the reference's shipped
 #: tables were measured on (no network here: the values of the published configs).
@@ -235,7 +253,47 @@ class Bench:
         return {name: round(statistics.median(v), 3) for name, v in per.items()}
 
 
-# ------------------------------------------------------------------ the two tables
+class MxBench(Bench):
+    """Bench over MXFP8 weights: copies of (fp8 e4m3 W, E8M0 scales [N, K/32]) quantized
+    from ~N(0, 1/K) bf16 weights, rotated through `rotate_bytes` of fp8; a path's check is
+    against the fp32 product of the same quantized bytes (the activation quantized by
+    `mxfp8.quant`, the rule both paths use)."""
+
+    def __init__(self, n: int, k: int, *, rotate_bytes: int = ROTATE_BYTES, seed: int = 0):
+        import torch  # noqa: PLC0415
+
+        from ..ops import mxfp8  # noqa: PLC0415
+
+        self.torch = torch
+        self.n, self.k = n, k
+        self.dev = torch.device("cuda", torch.cuda.current_device())
+        copies = max(2, -(-rotate_bytes // (n * k)))
+        free = torch.cuda.mem_get_info(self.dev)[0]
+        copies = max(2, min(copies, int(0.5 * free) // (n * k)))
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        self.ws = []
+        for _ in range(copies):
+            w = (torch.randn(n, k, device=self.dev, generator=g) * k ** -0.5).to(torch.bfloat16)
+            self.ws.append(mxfp8.quant(w))
+        self.g = g
+
+    def check(self, fn: Callable, x, out) -> float:
+        torch = self.torch
+        from ..ops import mxfp8  # noqa: PLC0415
+
+        got = fn(x, self.ws[0], out)
+        got = out if got is None else got
+        torch.cuda.synchronize()
+
+        def deq(q, s):
+            return q.float() * torch.pow(2.0, s.float() - 127.0).repeat_interleave(32, dim=-1)
+
+        xq, xs = mxfp8.quant(x)
+        ref = deq(xq, xs) @ deq(*self.ws[0]).t()
+        return float((got.float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+# ------------------------------------------------------------------ the tables
 
 
 def _template(schedule: Optional[str]) -> Callable:
@@ -329,10 +387,48 @@ def tune_linear(shapes: Dict[Tuple[int, int], str], ms: Sequence[int] = GRID, *,
     return out
 
 
+def tune_mxfp8(shapes: Dict[Tuple[int, int], str], ms: Sequence[int] = MX_GRID, *,
+               rounds: int = 5, min_gain: float = MIN_GAIN, rotate_bytes: int = ROTATE_BYTES,
+               log: Callable[[str], None] = print) -> Dict[str, dict]:
+    """The MXFP8 table's entries: per (N, K), hk's quant + MX GEMM against the same quant +
+    hipBLASLt's MX GEMM at each M."""
+    import torch  # noqa: PLC0415
+
+    from ..ops import mxfp8  # noqa: PLC0415
+
+    e8m0 = torch.float8_e8m0fnu
+
+    def engine_path(x, w, o):
+        q, s = mxfp8.quant(x)
+        if s.shape[0] % 128:
+            # hipBLASLt reads the activation's scales in whole 128-row blocks
+            s = torch.nn.functional.pad(s, (0, 0, 0, 128 - s.shape[0] % 128), value=127)
+        return torch._scaled_mm(q, w[0].t(), scale_a=s.view(e8m0), scale_b=w[1].view(e8m0),
+                                out_dtype=torch.bfloat16)
+
+    def hk_path(x, w, o):
+        q, s = mxfp8.quant(x)
+        return mxfp8.gemm(q, w[0], s, w[1], out=o)
+
+    out = {}
+    for (n, k), name in shapes.items():
+        bench = MxBench(n, k, rotate_bytes=rotate_bytes)
+        pts = []
+        for m in ms:
+            us = bench.time(m, {"engine": engine_path, "hk": hk_path}, rounds=rounds, log=log)
+            pts.append([m, us])
+            log(f"  {n}x{k} ({name}) M={m:5d}: {base_path(us, min_gain):9s} " +
+                "  ".join(f"{p} {v:.2f}" for p, v in us.items()))
+        out[f"{n}x{k}"] = entry(name, pts, min_gain)
+        del bench
+        torch.cuda.empty_cache()
+    return out
+
+
 def main(argv: Optional[Sequence[str]] = None) -> int:
     ap = argparse.ArgumentParser(prog="python -m hk.integration.tune", description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("kind", choices=("gemm", "vllm_linear"))
+    ap.add_argument("kind", choices=("gemm", "vllm_linear", "vllm_mxfp8"))
     ap.add_argument("--models", default=",".join(MODELS),
                     help="model names (of MODELS) or config.json paths, comma-separated")
     ap.add_argument("--tp", type=int, default=1)
@@ -351,7 +447,8 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
         print("no GPU: nothing to measure", file=sys.stderr)
         return 2
     arch = current_arch()
-    shapes = model_shapes(args.models.split(","), args.tp)
+    shapes = (dict(MX_SHAPES) if args.kind == "vllm_mxfp8"
+              else model_shapes(args.models.split(","), args.tp))
     if args.kind == "gemm":
         # the template's grid (gemm_cdna_routes.py NK): the models' (N, K), their gate and
         # up projections unmerged, and two squares
@@ -372,6 +469,12 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     if args.kind == "gemm":
         table = tune_gemm(sorted(shapes), ms or GEMM_MS, rounds=args.rounds or 3)
         table["arch"] = arch
+    elif args.kind == "vllm_mxfp8":
+        ents = tune_mxfp8(shapes, ms or MX_GRID, rounds=args.rounds or 5, min_gain=args.min_gain)
+        table = dict(kind="vllm_mxfp8", arch=arch, model="DeepSeek-V4.1-Flash (TP2) shapes",
+                     engine="mxfp8.quant + torch._scaled_mm (hipBLASLt MX)", tp=2,
+                     min_gain=args.min_gain, rounds=args.rounds or 5,
+                     rotate_mb=ROTATE_BYTES >> 20, **_where(), shapes=ents)
     else:
         ents = tune_linear(shapes, ms or GRID, rounds=args.rounds or 5, min_gain=args.min_gain)
         table = dict(kind="vllm_linear", arch=arch, model=args.models, engine="F.linear",

@@ -13,9 +13,12 @@ quantizes the activation (`mxfp8_e4m3_quantize`, AITER's per_1x32 rule) and call
   (`mxfp8.quant`, the same bits as vLLM's quantizer) and runs `mxfp8.gemm`; every other
   call runs vLLM's own quant and kernel.
 
-The route: N a multiple of 8 and K of 128 (the kernel's), and M >= MIN_M -- the reference's
-measured bound for its own kernel on the DeepSeek-V4.1 shapes (:35-36), used here until this
-build's kernel has a measured table of its own; `ENABLED = False` sends every call to vLLM.
+The route: N a multiple of 8 and K of 128 (the kernel's), then the measured table
+hk/tuned/routes_vllm_mxfp8_gfx950.json (`python -m hk.integration.tune vllm_mxfp8`; `$HK_VLLM_MXFP8_ROUTES`
+overrides it): for each measured (N, K), the Ms where hk's quant + MX GEMM beat the
+engine's by 3% (a shape it does not hold stays with vLLM, as the reference routes only the
+shapes it measured, :33-56). Without a table, M >= MIN_M, the reference's measured bound
+(:35-36). `ENABLED = False` sends every call to vLLM.
 """
 
 from __future__ import annotations
@@ -42,9 +45,34 @@ PATCH = engine.Op("hk_vllm::mxfp8_linear",
                   " -> Tensor", _fake, paths=("hk", "fallback"), graph="safe")
 
 
+ROUTES_ENV = "HK_VLLM_MXFP8_ROUTES"
+_TABLE: list = []
+
+
+def routes() -> Optional[engine.RouteTable]:
+    """The measured table for this process's arch (loaded once), or None."""
+    if not _TABLE:
+        from ..target import current_arch  # noqa: PLC0415
+
+        _TABLE.append(engine.shipped_table("vllm_mxfp8", current_arch(), ROUTES_ENV))
+    return _TABLE[0]
+
+
+def set_routes(table: Optional[engine.RouteTable]) -> None:
+    """Route by `table` from now on; None reloads the shipped one."""
+    _TABLE.clear()
+    if table is not None:
+        _TABLE.append(table)
+
+
 def schedule(m: int, n: int, k: int) -> bool:
     """Whether hk takes an M x N x K call."""
-    return ENABLED and n % 8 == 0 and k % 128 == 0 and m >= MIN_M
+    if not ENABLED or n % 8 or k % 128 or m < 1:
+        return False
+    t = routes()
+    if t is None:
+        return m >= MIN_M
+    return t.lookup(m, n, k) == "hk"
 
 
 _VLLM: list = []
@@ -130,7 +158,9 @@ def apply_patch() -> str:
     _ORIG_PWAL, _ORIG_APPLY = cls.process_weights_after_loading, cls.apply_weights
     cls.process_weights_after_loading = process_weights_after_loading
     cls.apply_weights = apply_weights
-    return f"mxfp8 -> hk for block-scaled layers at M >= {MIN_M}"
+    t = routes()
+    return ("mxfp8 -> hk where " + (f"{t.source} measured it faster" if t is not None
+                                    else f"M >= {MIN_M}"))
 
 
 def revert() -> str:
@@ -147,5 +177,5 @@ def status() -> str:
     return "not patched" if _ORIG_APPLY is None else PATCH.summary()
 
 
-__all__ = ["PATCH", "schedule", "mxfp8_linear", "apply_patch", "revert", "status",
+__all__ = ["PATCH", "schedule", "routes", "set_routes", "mxfp8_linear", "apply_patch", "revert", "status",
            "process_weights_after_loading", "apply_weights"]

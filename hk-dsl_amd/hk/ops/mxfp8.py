@@ -8,6 +8,8 @@ is gfx950's scaled one (v_mfma_scale_f32_32x32x64_f8f6f4), each lane passing the
 of its own fragment row and 32-K block; the scales reach LDS by the same DMA as the
 operands, 16 bytes a row every 8 half-stages (whole lines: one 4-byte load a row and
 half-stage doubled the L2 requests and cost 60%). K a multiple of 128, N of 8, any M.
+Where the tiles fill less than half the CUs, K is split over workgroups into fp32 shares
+(a cached workspace, `_native.workspace`) that a second pass sums in split order.
 
 `quant(x)` is the activation side (python/hk/ops/mxfp8.py:605-660): bf16 x to fp8 e4m3 and
 E8M0 scales by AITER's per_1x32 rule (python/hk/mx.py:17-31), in one launch, the scales in
@@ -60,10 +62,13 @@ def gemm(a, b, sa, sb, out=None):
         out = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(1) != 1:
         raise ValueError(f"mxfp8.gemm: out is bf16 ({m}, {n}) with unit column stride")
-    nat.check(nat.lib().hkx_mx_gemm(
+    L = nat.lib()
+    nws = L.hkx_mx_gemm_workspace(m, n, k)
+    ws = nat.workspace(a.device, nws)
+    nat.check(L.hkx_mx_gemm(
         a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), sa.data_ptr(), sa.stride(0),
         sb.data_ptr(), sb.stride(0), out.data_ptr(), out.stride(0), m, n, k,
-        nat.stream_of(a.device)))
+        ws.data_ptr() if ws is not None else None, nws, nat.stream_of(a.device)))
     return out
 
 

@@ -36,6 +36,9 @@
  *   hkx_gemm_workspace  gemm_cdna_dp.scratch_for / decode_gemm.scratch_for
  *                       (gemm_cdna_dp.py:330-338, decode_gemm.py:283-298): the size of
  *                       the fp32 share buffer a plan needs (the caller allocates it).
+ *   hkx_mx_gemm_workspace  the same for hkx_mx_gemm's split-K shares (this build splits
+ *                       K across workgroups where the reference's MX kernel runs few tiles
+ *                       unsplit, python/hk/ops/mxfp8.py:64-110).
  *   hkx_last_error      the message the reference raises in Python (ValueError /
  *                       TypeError texts of templates/gemm.py:770-803).
  */
@@ -49,7 +52,7 @@
 extern "C" {
 #endif
 
-#define HKX_ABI_VERSION 2
+#define HKX_ABI_VERSION 3
 
 /* Status codes. */
 #define HKX_OK 0
@@ -238,10 +241,15 @@ int hkx_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
  * (N, K/32) E8M0 bytes (scale 2^(s - 127) for its row and 32 K), row strides lda, ldb,
  * ldc in elements and sa_ld, sb_ld in bytes. K a multiple of 128, N of 8; sa and sb
  * 4-byte aligned with sa_ld, sb_ld multiples of 4 and >= K/32; C's rows 16-byte aligned.
- * M any. */
+ * M any. Where the 256 x 256 tiles fill less than half the CUs and K is 2048 or more, K is
+ * split over workgroups (1024 K or more each, at most 8) into fp32 shares in ws (hkx_mx_gemm_workspace() bytes; HKX_ERR_WORKSPACE if
+ * smaller), summed in split order by a second pass. */
 int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const uint8_t* sa,
                 int64_t sa_ld, const uint8_t* sb, int64_t sb_ld, void* c, int64_t ldc,
-                int32_t m, int32_t n, int32_t k, void* stream);
+                int32_t m, int32_t n, int32_t k, void* ws, size_t ws_bytes, void* stream);
+
+/* Bytes of fp32 workspace hkx_mx_gemm needs at M x N x K (0 if it runs in one pass). */
+size_t hkx_mx_gemm_workspace(int32_t m, int32_t n, int32_t k);
 
 /* x bf16 (M, K) -> q fp8-e4m3 (M, K) and s (M, K/32) E8M0 bytes: per 32-column block,
  * e = ceil(log2(amax / 448)) with amax >= 2^-126, q = x / 2^e rounded to nearest even,

@@ -27,7 +27,7 @@ def test_the_library_exports_every_declared_symbol():
     assert set(names) == set(nat.SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.hkx_abi_version() == 2
+    assert L.hkx_abi_version() == 3
 
 
 def test_no_kernel_launch_stub_is_missing():
@@ -133,6 +133,22 @@ def test_workspace_sizes():
     assert L.hkx_gemm_workspace(ctypes.byref(sk)) == 0
     sk.variant = nat.RING_STREAMK | nat.RING_WAVESPLIT
     assert _check(sk)[0] == nat.ERR_ARG
+
+
+def test_mx_workspace_sizes():
+    """The MX GEMM splits K where its 256 x 256 tiles fill less than half of (this host's
+    assumed) 256 CUs: min(CUs / tiles, k-tiles / 8, 8) splits, trimmed so none is empty."""
+    L = nat.lib()
+    ws = L.hkx_mx_gemm_workspace
+    assert ws(4096, 4096, 4096) == 0                       # 256 tiles: one pass
+    assert ws(2048, 1792, 5120) == 4 * 2048 * 1792 * 4     # 56 tiles, 40 k-tiles: 4 splits
+    assert ws(300, 512, 2048) == 2 * 300 * 512 * 4         # 16 k-tiles: 2 splits of 8
+    assert ws(64, 512, 4224) == 4 * 64 * 512 * 4           # 33 k-tiles: 9, 9, 9 and 6
+    assert ws(300, 512, 1152) == 0                         # 9 k-tiles: too few to split
+    # a split call refuses to run without its workspace (checked before any launch)
+    p = 1 << 20
+    rc = L.hkx_mx_gemm(p, 5120, p, 5120, p, 160, p, 160, p, 1792, 2048, 1792, 5120, None, 0, None)
+    assert rc == nat.ERR_WORKSPACE and b"workspace" in L.hkx_last_error()
 
 
 def test_the_build_refuses_spills():

@@ -158,12 +158,26 @@ def test_patch_contracts():
 
 
 def test_vllm_mxfp8_route_and_patch_without_vllm():
-    """The MXFP8 route takes whole shapes at M >= MIN_M only, and the patch reports, rather
-    than fails, where vLLM is absent (vllm_mxfp8.py:191-200's contract)."""
+    """The MXFP8 route: a measured table's runs where there is one (unmeasured shapes stay
+    with vLLM), else M >= MIN_M; and the patch reports, rather than fails, where vLLM is
+    absent (vllm_mxfp8.py:191-200's contract)."""
+    from hk.integration import engine as E
     from hk.integration import vllm_mxfp8 as V
 
-    assert V.schedule(V.MIN_M, 5120, 4096)
-    assert not V.schedule(V.MIN_M - 1, 5120, 4096)
+    # without a table: M >= MIN_M
+    V.set_routes(None)
+    V._TABLE.append(None)
+    try:
+        assert V.schedule(V.MIN_M, 5120, 4096)
+        assert not V.schedule(V.MIN_M - 1, 5120, 4096)
+        # with one: its runs, and unmeasured shapes stay with vLLM
+        V.set_routes(E.RouteTable({(5120, 4096): {"runs": [[16, 256, "hk"], [384, 384, "fallback"],
+                                                           [512, 8192, "hk"]]}}))
+        assert V.schedule(16, 5120, 4096) and V.schedule(9000, 5120, 4096)
+        assert not V.schedule(384, 5120, 4096) and not V.schedule(8, 5120, 4096)
+        assert not V.schedule(4096, 2048, 4096)  # not measured
+    finally:
+        V.set_routes(None)
     assert not V.schedule(4096, 5124, 4096)   # N % 8
     assert not V.schedule(4096, 5120, 4000)   # K % 128
     V.ENABLED = False

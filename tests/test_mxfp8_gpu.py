@@ -30,11 +30,14 @@ def _operands(m, n, k, seed, block_weight_scales=False):
 @pytest.mark.parametrize("m,n,k,blk", [(256, 256, 512, True), (512, 384, 1280, True),
                                        (300, 512, 1152, False), (1, 256, 128, False),
                                        (2100, 2048, 2048, False), (4096, 4352, 128, False),
-                                       (4096, 4352, 1152, True)])
+                                       (4096, 4352, 1152, True), (64, 512, 4224, False),
+                                       (16, 1792, 5120, True)])
 def test_mx_gemm_matches_the_scaled_product(m, n, k, blk):
     """Whole and partial chunks of 8 half-stages of scales (K = 1152: 18 half-stages, its last
     chunk two), the shortest K (128: a two-half-stage chunk a tile, two tiles a workgroup at
-    4096 x 4352), ragged M."""
+    4096 x 4352), ragged M; K split over workgroups where the tiles are few (2 splits at
+    2100 x 2048 x 2048, 5 at 16 x 1792 x 5120, 4 of 9, 9, 9 and 6 k-tiles at 64 x 512 x
+    4224), each split's scales read from its own first K block."""
     a, b, sa, sb = _operands(m, n, k, seed=m + n + k, block_weight_scales=blk)
     print(f"case mx_gemm {m}x{n}x{k}", flush=True)
     out = mxfp8.gemm(a.to(DEV), b.to(DEV), sa.to(DEV), sb.to(DEV))
@@ -92,11 +95,21 @@ def test_mx_linear_is_quant_then_gemm():
 
 
 def test_vllm_mxfp8_op_takes_the_hk_path():
-    """hk_vllm::mxfp8_linear's body at M >= MIN_M on a 32 x 32 block-scaled weight: this
-    build's quant and GEMM, right against the oracle (no vLLM needed on that path)."""
+    """hk_vllm::mxfp8_linear's body where the route takes the shape (a table that routes it),
+    on a 32 x 32 block-scaled weight: this build's quant and GEMM, right against the oracle
+    (no vLLM needed on that path)."""
+    from hk.integration import engine as E
     from hk.integration import vllm_mxfp8 as V
 
-    m, n, k = V.MIN_M, 512, 1024
+    m, n, k = 2048, 512, 1024
+    V.set_routes(E.RouteTable({(n, k): {"runs": [[1, 8192, "hk"]]}}))
+    try:
+        _vllm_op(V, m, n, k)
+    finally:
+        V.set_routes(None)
+
+
+def _vllm_op(V, m, n, k):
     x = _x(m, k, seed=11)
     g = torch.Generator().manual_seed(12)
     w = torch.randn(n, k, generator=g).to(torch.float8_e4m3fn)

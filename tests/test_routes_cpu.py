@@ -98,3 +98,30 @@ def test_shipped_vllm_table_is_its_own_decision():
             assert t.lookup(m, n, k) == tune.base_path(times, d["min_gain"])
     # decode-sized M on the K = 4096 shapes goes to the decode kernel
     assert t.lookup(1, 4096, 4096) == "hk_decode" and t.lookup(16, 24576, 4096) == "hk_decode"
+
+
+def test_shipped_mxfp8_table_is_its_own_decision():
+    """The MXFP8 table (hk's quant + MX GEMM against the same quant + hipBLASLt's MX GEMM):
+    every run is what its points decide, the route reads it, and a point where the engine
+    failed its check (no engine time) goes to hk."""
+    from hk.integration import vllm_mxfp8 as V
+
+    path = TUNED / "routes_vllm_mxfp8_gfx950.json"
+    d = json.loads(path.read_text())
+    assert d["arch"] == "gfx950" and d["kind"] == "vllm_mxfp8"
+    assert {tuple(int(v) for v in key.split("x")) for key in d["shapes"]} == set(tune.MX_SHAPES)
+    t = engine.RouteTable.from_json(path)
+    V.set_routes(t)
+    try:
+        for key, ent in d["shapes"].items():
+            rs, _ = tune.runs(ent["points"], d["min_gain"])
+            assert ent["runs"] == rs, key
+            n, k = (int(v) for v in key.split("x"))
+            for m, times in ent["points"]:
+                want = tune.base_path(times, d["min_gain"])
+                assert t.lookup(m, n, k) == want
+                assert V.schedule(m, n, k) == (want == "hk")
+                if "engine" not in times:
+                    assert want == "hk"
+    finally:
+        V.set_routes(None)
