@@ -220,7 +220,7 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
     if (sc == HKX_TILE_PINGPONG && !pp_ok)
       return fail(HKX_ERR_ARG, "the ping-pong tile kernel takes 256x256 tiles");
-    if (sc == HKX_TILE_RING ? (a->variant & ~(HKX_RING_WAVESPLIT | HKX_RING_STREAMK)) != 0 ||
+    if (sc == HKX_TILE_RING ? (a->variant & ~(HKX_RING_WAVESPLIT | HKX_RING_STREAMK | HKX_RING_HALFSTAGE)) != 0 ||
                                   (a->variant & HKX_RING_WAVESPLIT && a->variant & HKX_RING_STREAMK)
                             : (a->variant & ~(HKX_PP_MFMA32 | HKX_PP_ONE_TILE)) != 0 ||
                                   (a->variant && sc != HKX_TILE_PINGPONG))
@@ -354,6 +354,8 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
   if (p.schedule == HKX_TILE_RING && hkx::ring_takes(t, fp8, mode)) {
     dim3 g = grid;
     g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
+    if (!(p.variant & HKX_RING_HALFSTAGE) && grid.y == 1 && hkx::quad_takes(t, fp8, mode))
+      return hkx::launch_quad(t, mode, g, s);
     return hkx::launch_ring(t, fp8, mode, g, s);
   }
   if (p.schedule == HKX_TILE_RING) return hkx::launch_pp(t, fp8, mode, true, grid, s);

@@ -1,0 +1,337 @@
+// The quadrant ring GEMM kernel: bf16 C (M, N) = act(A . B^T (+ bias)) on 256 x 256 tiles,
+// one persistent workgroup of 8 waves a CU, fills of whole 128-byte lines.
+//
+// Replaces, for bf16 operands and a 16-bit C with no epilogue or a bias and an activation,
+// the reference's pp kernel (python/hk/ops/gemm_cdna.py:57-586, HipKittens' 256 x 256 x 64
+// eight-wave ping-pong); the ring kernel (hkx_ring.hpp) takes every other form.
+//
+// * Quadrants. A tile's A rows are two halves of 128 (A0, A1), its B rows likewise (B0,
+//   B1). Wave w of the 2 x 4 grid (r, c) = (w / 4, w % 4) owns rows 64 r + 128 i and
+//   columns 32 c + 128 j of the tile for i, j in {0, 1}: four 64 x 32 accumulator blocks,
+//   one per (A half i, B half j). So each half of A or B is read by all eight waves in one
+//   phase and is free for its next fill right after.
+// * K-tiles of 64 (whole 128-byte lines of a row). LDS holds two K-tile slots of four
+//   quarters (A0, A1, B0, B1), 16 KB each. A quarter is 16 blocks of 1 KB, block b the 8
+//   rows 8 b ..: its first 512 bytes K 0-31 of the 8 rows (64 bytes a row), the second K
+//   32-63. One fill instruction moves one block: lanes l and l + 32 fetch the two halves
+//   of row l % 32 / 4's line, so every request is a whole line, and the 64-byte K-halves
+//   keep the bank pattern of 64-byte rows (16-byte chunk c of row r at c ^ swz4(r)).
+// * Phases. Per K-tile t, four phases, each: LDS reads into registers, one fill (the
+//   wave's 2 KB share of a quarter), a barrier, 16 MFMAs (v_mfma_f32_16x16x32_bf16), a
+//   barrier:
+//     1: read A0(t) and B0(t); fill A1(t + 1);  math (0, 0)
+//     2: read B1(t);           fill B0(t + 2);  math (0, 1)
+//     3: read A1(t);           fill A0(t + 2);  math (1, 0)
+//     4:                       fill B1(t + 2);  math (1, 1)
+//   A quarter is refilled only in a phase after both groups read it (group 1 runs one
+//   barrier behind group 0, so its reads of phase k land under group 0's MFMAs of phase
+//   k); each fill is 5-7 phases ahead of its first read. Before each barrier a wave waits
+//   for all but its 10 newest fill instructions: in issue order the five quarters after
+//   the one the next phase reads.
+// * Tiles follow one another without a break in the fills (K-tile indices run on across
+//   the workgroup's tiles); the epilogue stores from the accumulators after the tile's
+//   last phase. A tile's bias reaches LDS by DMA during the tile before it (three slots
+//   by tile), so the epilogue's reads wait for no fill.
+//
+// The paired form (C = silu(gate) * up, B's gate and up rows pair_off apart) reads 64 gate
+// and 64 up rows a B quarter, so a wave's two 16-row B fragments of a block are the gate
+// and up rows of the same 16 C columns; a tile is 128 C columns.
+//
+// Ragged M and N read zeros through the operands' buffer bounds; C's stores are dropped
+// past M by its buffer bound and predicated on n < N (N % 8 == 0).
+#pragma once
+
+#include "hkx_ring.hpp"
+
+namespace hkx {
+
+template <int ACT, int EPF, bool PAIR = false>
+__global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
+  constexpr int BM = 256, BN = PAIR ? 128 : 256;  // BN: C columns of a tile
+  constexpr int QB = 128 * 128;       // one quarter: 128 rows x 128 bytes
+  constexpr int BIAS = 8 * QB;        // then the bias: [tile % 3][1 KB]
+  constexpr int SMEM = BIAS + 3 * 1024;
+  static_assert(EPF == kEpNone || EPF == kEpBias, "forms");
+  static_assert(!PAIR || (EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;  // the ping-pong group and the wave's grid row
+  const int wc = wave & 3;
+
+  const int total = p.tiles_m * p.tiles_n;
+  const int G = gridDim.x;
+  const int my_tiles = (total - (int)blockIdx.x + G - 1) / G;
+  const int nkt = p.kt_total;     // K-tiles of 64 a tile
+  const int nu = my_tiles * nkt;  // K-tiles of this workgroup
+
+  // tile (m0, n0) of local tile lt: the ring kernel's XCD-chunked grouped raster
+  auto tile_at = [&](int lt, int& m0, int& n0) {
+    const int v = (int)blockIdx.x + lt * G;
+    int L = v;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    const int per = p.wgm * p.tiles_n;
+    const int gi = L / per;
+    const int first = gi * p.wgm;
+    const int gm = min(p.tiles_m - first, p.wgm);
+    const int in = L - gi * per;
+    m0 = (first + in % gm) * BM;
+    n0 = (in / gm) * BN;
+  };
+
+  // ---- fills. Instruction k (0, 1) of wave w moves block 2 w + k of a quarter (rows
+  // 16 w + 8 k + [0, 8)); lane l fetches row 16 w + 8 k + l % 32 / 4, K-half l / 32, its
+  // 16-byte chunk (l % 4) ^ swz4(row) -- swz4 of those rows is (w & 1) | (k << 1).
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b, p.b_bytes);
+  // Paired (gate | up, B has 2N rows): B tile row 16 F + x is row x of the gate (F even) or
+  // up (F odd) block of C columns 16 (F / 2) ..: quarter h's row 16 w + x, F = 8 h + w, is
+  // B row n0 + 64 h + 16 (w / 2) + x (+ pair_off for odd w).
+  uint32_t lrow[2], lrow_b[2], lch[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    lrow[k] = (uint32_t)(16 * wave + 8 * k + (lane & 31) / 4);
+    lrow_b[k] = PAIR ? (uint32_t)(16 * (wave >> 1) + 8 * k + (lane & 31) / 4 +
+                                  ((wave & 1) ? p.pair_off : 0))
+                     : lrow[k];
+    lch[k] = (uint32_t)(64 * (lane >> 5) + 16 * ((lane & 3) ^ ((wave & 1) | (k << 1))));
+  }
+  // Two fill streams walk the workgroup's K-tiles: one a K-tile ahead (A1 of t + 1), one
+  // two ahead (B0, A0, B1 of t + 2); each keeps its K-tile's index, position in its tile
+  // and tile origin. Past the last K-tile a stream stays on it: its fills fetch the same
+  // bytes again into the slot that K-tile already holds.
+  struct Stream {
+    int g, t, lt, m0, n0;
+  };
+  auto stream_at = [&](int g0) {
+    Stream s{0, 0, 0, 0, 0};
+    s.g = min(g0, nu - 1);
+    s.lt = s.g / nkt;
+    s.t = s.g - s.lt * nkt;
+    tile_at(s.lt, s.m0, s.n0);
+    return s;
+  };
+  auto advance = [&](Stream& s) {
+    if (s.g + 1 >= nu) return;
+    ++s.g;
+    if (++s.t == nkt) {
+      s.t = 0;
+      tile_at(++s.lt, s.m0, s.n0);
+    }
+  };
+  // quarter q (0 A0, 1 A1, 2 B0, 3 B1) of stream s's K-tile into slot g & 1
+  auto fill = [&](int q, const Stream& s) {
+    const bool isb = q >= 2;
+    const uint32_t ld = isb ? p.ldb_b : p.lda_b;
+    const uint32_t row0 = (uint32_t)((isb ? s.n0 : s.m0) + (isb && PAIR ? 64 : 128) * (q & 1));
+    const uint32_t so = __builtin_amdgcn_readfirstlane(row0 * ld + (uint32_t)s.t * 128u);
+    uint8_t* base = smem + ((s.g & 1) * 4 + q) * QB + wave * 2048;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      buf_load16_lds(isb ? rb : ra, base + k * 1024, (isb ? lrow_b[k] : lrow[k]) * ld + lch[k], so);
+  };
+
+  // ---- the bias of local tile lt: 256 bf16 by 16-byte DMA from wave 0 into slot lt % 3
+  // (lanes 32-63 read past the tile's 512 bytes into the slot's spare half). Three slots:
+  // the DMA of tile lt + 1, at tile lt's first phase, runs while group 1 may still read
+  // tile lt - 1's.
+  constexpr bool bias = EPF == kEpBias;
+  const __amdgpu_buffer_rsrc_t rbias =
+      make_rsrc(bias ? p.ep.ra.p : nullptr, bias ? (uint32_t)p.N * 2u : 0u);
+  auto bias_load = [&](int lt) {
+    if (!bias || wave != 0) return;
+    int m0, n0;
+    tile_at(lt, m0, n0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rbias, (__attribute__((address_space(3))) void*)(smem + BIAS + (lt % 3) * 1024), 16,
+        (uint32_t)lane * 16u, __builtin_amdgcn_readfirstlane((uint32_t)n0 * 2u), 0, 0);
+  };
+
+  // ---- fragment reads (16 x 16 x 32: lane l reads row l % 16 of a 16-row fragment,
+  // 16-byte chunk l / 16 of the K-half). A fragment of quarter rows r0.. (r0 % 16 == 0)
+  // at K-half s sits at r0 * 128 + s * 512 + rdo[(r0 >> 4) & 1].
+  uint32_t rdo[2];
+  {
+    const int rr = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+      rdo[par] = (uint32_t)((rr >> 3) * 1024 + (rr & 7) * 64 + ((q ^ (par | ((rr >> 3) << 1))) << 4));
+  }
+  bf16x8 af[4][2], bf0[2][2], bf1[2][2];  // [fragment][K-half]
+  auto read_a = [&](int slot, int i) {
+    const uint8_t* s = smem + (slot * 4 + i) * QB;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int r0 = grp * 64 + 16 * f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) af[f][h] = *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[f & 1]);
+    }
+  };
+  auto read_b = [&](int slot, int j, bf16x8 (&bf)[2][2]) {
+    const uint8_t* s = smem + (slot * 4 + 2 + j) * QB;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int r0 = wc * 32 + 16 * g;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) bf[g][h] = *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[g & 1]);
+    }
+  };
+
+  f32x4 acc[2][2][4][2];  // [A half][B half][row fragment][column fragment]
+  auto math = [&](int i, int j, const bf16x8 (&bf)[2][2], bool zero) {
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const f32x4 c = (zero && h == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j][f][g];
+          acc[i][j][f][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[g][h], af[f][h], c, 0, 0, 0);
+        }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // ---- the epilogue of local tile lt from the accumulators. Lane l (row l % 16, quarter
+  // q = l / 16) holds columns 4 q + [0, 4) of each 16-column fragment; the two fragments
+  // of a 32-column block trade quarters (v_permlane16_swap) so each lane stores 16
+  // contiguous bytes.
+  const uint32_t row_b = (uint32_t)p.ldc * 2u;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c, (uint32_t)p.M * row_b);
+  auto epilogue = [&](int lt) {
+    int m0, n0;
+    tile_at(lt, m0, n0);
+    const int rf = lane & 15, q = lane >> 4;
+    [[maybe_unused]] f32x4 bv[2][2];
+    if constexpr (bias) {
+      const uint32_t* bs = (const uint32_t*)(smem + BIAS + (lt % 3) * 1024);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const int col = 128 * j + 32 * wc + 16 * g + 4 * q;  // even: a whole word pair
+          bv[j][g] = unpack_bf16x4(*(const u32x2*)(bs + col / 2));
+        }
+    }
+    if constexpr (PAIR) {
+      // fragment 0 of a block holds the gate rows, fragment 1 the up rows of C columns
+      // 64 j + 16 c + [0, 16): lane l's four at 4 q
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            __builtin_amdgcn_sched_barrier(0);
+            const u32x2 w = pack4<2>(HKX_BF16, silu_mul4(acc[i][j][f][0], acc[i][j][f][1]));
+            const int n = 64 * j + 16 * wc + 4 * q;
+            const int ml = 128 * i + 64 * grp + 16 * f + rf;
+            if (n0 + n < p.N)
+              __builtin_amdgcn_raw_buffer_store_b64(w, rc, (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u,
+                                                    0, 0);
+          }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ca = 128 * j + 32 * wc;  // the block's first column
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          __builtin_amdgcn_sched_barrier(0);
+          f32x4 va = acc[i][j][f][0], vb = acc[i][j][f][1];
+          if constexpr (bias) {
+            va += bv[j][0];
+            vb += bv[j][1];
+          }
+          va = act4c<ACT>(0, va);
+          vb = act4c<ACT>(0, vb);
+          const u32x2 wa = pack4<2>(HKX_BF16, va), wb = pack4<2>(HKX_BF16, vb);
+          uint32_t x0 = wa.x, x1 = wb.x, y0 = wa.y, y1 = wb.y;
+          swap16(x0, x1);
+          swap16(y0, y1);
+          const int n = ca + 16 * (q & 1) + 8 * (q >> 1);
+          const int ml = 128 * i + 64 * grp + 16 * f + rf;
+          if (n0 + n < p.N)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                i32x4{(int)x0, (int)y0, (int)x1, (int)y1}, rc,
+                (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u, 0, 0);
+        }
+      }
+  };
+
+  // ---- the K loop. Before the first phase: K-tile 0 whole and K-tile 1 but A1, in the
+  // order the steady state issues them (B0, A0, B1 of t + 2 in phases 2-4 of t, A1 of t + 1
+  // in phase 1 of t).
+  auto sync_mem = [&]() {  // before a math phase: this wave's LDS reads landed
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(10));
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto sync_math = [&]() {  // before a memory phase: the quarter it reads landed everywhere
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(wait_vm(10));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  bias_load(0);
+  Stream s1 = stream_at(0), s2 = stream_at(0);
+  fill(2, s2);
+  fill(0, s2);
+  fill(3, s2);
+  fill(1, s1);
+  advance(s1);
+  advance(s2);
+  fill(2, s2);
+  fill(0, s2);
+  fill(3, s2);
+  advance(s2);
+  __builtin_amdgcn_s_waitcnt(wait_vm(10));  // A0 and B0 of K-tile 0
+  __builtin_amdgcn_s_barrier();
+  if (grp == 1) __builtin_amdgcn_s_barrier();
+  int g = 0;
+  for (int lt = 0; lt < my_tiles; ++lt) {
+    for (int t = 0; t < nkt; ++t, ++g) {
+      const int slot = g & 1;
+      const bool z = t == 0;
+      // phase 1
+      read_a(slot, 0);
+      read_b(slot, 0, bf0);
+      if (t == 0 && lt + 1 < my_tiles) bias_load(lt + 1);
+      fill(1, s1);
+      advance(s1);
+      sync_mem();
+      math(0, 0, bf0, z);
+      sync_math();
+      // phase 2
+      read_b(slot, 1, bf1);
+      fill(2, s2);
+      sync_mem();
+      math(0, 1, bf1, z);
+      sync_math();
+      // phase 3
+      read_a(slot, 1);
+      fill(0, s2);
+      sync_mem();
+      math(1, 0, bf0, z);
+      sync_math();
+      // phase 4
+      fill(3, s2);
+      advance(s2);
+      sync_mem();
+      math(1, 1, bf1, z);
+      sync_math();
+    }
+    epilogue(lt);
+  }
+  if (grp == 0) __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no fill lands in LDS after the exit
+}
+
+}  // namespace hkx

@@ -29,7 +29,7 @@ ACT_NONE, ACT_GELU_TANH, ACT_SILU, ACT_RELU = range(4)
 KERNEL_AUTO, KERNEL_TILE, KERNEL_DECODE = range(3)
 TILE_AUTO, TILE_PINGPONG, TILE_W4, TILE_W8, TILE_RING = range(5)
 PP_MFMA32, PP_ONE_TILE = 1, 2
-RING_WAVESPLIT, RING_STREAMK = 4, 8
+RING_WAVESPLIT, RING_STREAMK, RING_HALFSTAGE = 4, 8, 16
 #: The tile schedules by name (the route candidates' "schedule").
 #: HKX_KERNEL_DECODE variant bit: the streaming kernel where it takes the call.
 DEC_STREAM = 1

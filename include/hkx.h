@@ -178,6 +178,12 @@ typedef struct HkxEpilogue {
                                 and applies the epilogue) -- the reference's dp+sk stream-K
                                 mode (gemm_cdna.py:421-496, 635-729) without its in-kernel
                                 fix-up; hkx_gemm_workspace() sizes the shares */
+#define HKX_RING_HALFSTAGE 16 /* every form on the half-stage ring kernel. Without it a call the
+                                 quadrant kernel takes runs there (bf16 operands and C, no
+                                 split, no epilogue or a bf16 bias and an activation): each
+                                 wave's output spread over the tile's four 128 x 128 quadrants,
+                                 whole 128-byte lines a fill -- the reference's pp schedule
+                                 (gemm_cdna.py:57-586). Combines with the two bits above */
 
 /* HKX_KERNEL_DECODE variant bits. */
 #define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K a multiple

@@ -420,3 +420,47 @@ def test_ring_wave_split(form, variant):
         resd, rsd = res.to(DEV), rs.to(DEV)
         _run(a.to(DEV), b.to(DEV), c, ep=_fused([(rsd, nat.COL), (resd, nat.TILE)], cs=0, ta=1), **kw)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["quad", "halfstage"])
+@pytest.mark.parametrize("form", ["plain", "bias", "bias_gelu", "silu", "silu_mul"])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 520, 128), (4096, 4352, 192),
+                                 (1000, 2048, 1088), (2048, 9216, 512)])
+def test_ring_quad(form, mnk, half):
+    """The quadrant kernel (the ring schedule's default for these forms) and, with
+    HKX_RING_HALFSTAGE, the half-stage ring kernel on the same calls: one K-tile a tile
+    (its fills run on into the next tile), ragged M and N, 272 tiles on 256 workgroups
+    (some walk two), K-tiles past what two LDS slots hold; with wave split (the rest of N
+    on 128 x 256 tiles) at 2048 x 9216; the paired silu * up form (128 C columns a tile,
+    gate and up rows N apart). Its wait counts and fill order run on K-tile counts 1-17."""
+    m, n, k = mnk
+    variant = (nat.RING_HALFSTAGE if half else 0) | (nat.RING_WAVESPLIT if n == 9216 else 0)
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, variant=variant)
+    if form == "silu_mul":  # B holds the gate rows, then the up rows
+        a, b = _data(m, 2 * n, k, seed=62)
+        acc = O.gemm_fp32(a, b)
+        c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+        ep = nat.HkxEpilogue()
+        ep.form = nat.EP_SILU_MUL
+        _run(a.to(DEV), b.to(DEV), c, ep=ep, **kw)
+        O.assert_close(c, O.silu_and_mul(acc[:, :n], acc[:, n:]), rtol=1e-2, atol=1e-2)
+        return
+    a, b = _data(m, n, k, seed=60)
+    acc = O.gemm_fp32(a, b)
+    g = torch.Generator().manual_seed(61)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    if form == "plain":
+        ref = acc
+        _run(a.to(DEV), b.to(DEV), c, **kw)
+    elif form == "bias":
+        ref = acc + bias.float()
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0), **kw)
+    elif form == "bias_gelu":
+        ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
+    else:
+        ref = O.silu(acc)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([], act=nat.ACT_SILU), **kw)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
