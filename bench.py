@@ -161,6 +161,7 @@ def main():
     import torch
 
     import hk
+    from hk import _native as nat
 
     dev = "cuda:0"
     T = hk.templates.gemm
@@ -179,7 +180,12 @@ def main():
     achieved = flops / mean_s / 1e12
     plan = T.plan(m, n, k)
     sched = plan[0].sched.get("schedule")
-    kname = {"ring": "hkx::ring_kernel<bf16, kStore16, GELU_TANH, kEpBias>",
+    variant = plan[0].sched.get("variant", 0) or 0
+    # the ring schedule runs this form (bf16, a bias and an activation) on the quadrant
+    # kernel unless the half-stage ring is asked for
+    ring = ("hkx::ring_kernel<bf16, kStore16, GELU_TANH, kEpBias>" if variant & nat.RING_HALFSTAGE
+            else "hkx::quad_kernel<GELU_TANH, kEpBias>")
+    kname = {"ring": ring,
              "pp": "hkx::pp_kernel<bf16, kStore16, GELU_TANH, mfma16>",
              "w4": "hkx::tile4_kernel<256, 256, bf16, kStore16, GELU_TANH>"}.get(sched, str(sched))
     res = {
@@ -198,7 +204,7 @@ def main():
     }
     # HBM bytes a launch of this kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     # runs summarised under profiles/ (null if they were taken on another kernel)
-    tr = os.path.join(ROOT, "profiles", "traffic_ring_bias_gelu_cfg2.json")
+    tr = os.path.join(ROOT, "profiles", "traffic_quad_bias_gelu_cfg2.json")
     if os.path.isfile(tr):
         with open(tr) as f:
             rec = json.load(f)
