@@ -37,11 +37,12 @@ bool ring_takes(const TileArgs& a, bool fp8, int mode);
 hipError_t launch_ring(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
 hipError_t launch_ring_bf16(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
 hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
-// The quadrant ring kernel (hkx_quad.hpp): bf16 operands and C, no split; no epilogue or a
-// unit-stride 16-byte aligned bf16 bias with an activation, or the paired silu * up form;
-// quad_takes says which.
+// The quadrant ring kernel (hkx_quad.hpp): a 16-bit bf16 C, no split; bf16 operands with no
+// epilogue, a bias and an activation, or the paired silu * up form; fp8 operands with no
+// epilogue or the dequant forms (row and column fp32 scales, a bf16 bias). Vectors of unit
+// stride, 16-byte aligned; quad_takes says which calls.
 bool quad_takes(const TileArgs& a, bool fp8, int mode);
-hipError_t launch_quad(const TileArgs& a, int mode, dim3 grid, hipStream_t s);
+hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
 // The MX form (fp8 operands, E8M0 block scales in a.sa / a.sb), no epilogue: bf16 C, or
 // fp32 shares of a K split (f32_shares, a.c the workspace, grid.y the splits).
 hipError_t launch_ring_mx(const TileArgs& a, bool f32_shares, dim3 grid, hipStream_t s);

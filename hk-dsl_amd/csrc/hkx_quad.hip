@@ -1,22 +1,40 @@
 // The quadrant ring GEMM kernel (hkx_quad.hpp): which calls it takes, its instantiations.
+#include <type_traits>
 #include "hkx_launch.hpp"
 #include "hkx_quad.hpp"
 
 namespace hkx {
 
-bool quad_takes(const TileArgs& a, bool fp8, int mode) {
-  if (fp8 || (mode != kStore16 && mode != kPair16) || a.c_dt != HKX_BF16 ||
-      a.kt_split < a.kt_total)
-    return false;
-  if (!ring_takes(a, fp8, mode)) return false;
-  if (mode == kPair16) return true;
+namespace {
+
+bool vec16_16(const Opnd& o) { return o.p && o.dt == HKX_BF16 && o.ld == 1 && ((uintptr_t)o.p & 15) == 0; }
+bool vec32_16(const Opnd& o) { return o.p && o.dt == HKX_FP32 && o.ld == 1 && ((uintptr_t)o.p & 15) == 0; }
+
+// The compiled epilogue form the quadrant kernel runs a call with, or -1 if it does not
+// take the call. Vector operands reach LDS by 16-byte DMA: unit stride, 16-byte aligned.
+int quad_form(const TileArgs& a, bool fp8, int mode) {
+  if ((mode != kStore16 && mode != kPair16) || a.c_dt != HKX_BF16 || a.kt_split < a.kt_total)
+    return -1;
+  if (!ring_takes(a, fp8, mode)) return -1;
+  if (mode == kPair16) return fp8 ? -1 : kEpNone;
   const Fused& e = a.ep;
-  if (e.form == HKX_EP_NONE) return true;
-  if (e.form != HKX_EP_FUSED || e.ta.p || e.cs.p || e.rs.p || e.cmul != 1.0f || e.cadd != 0.0f)
-    return false;
-  // a bf16 bias of unit stride, 16-byte aligned (its DMA moves 16 bytes a lane), or none
-  return !e.ra.p || (e.ra.dt == HKX_BF16 && e.ra.ld == 1 && ((uintptr_t)e.ra.p & 15) == 0);
+  if (e.form == HKX_EP_NONE) return kEpNone;
+  if (e.form != HKX_EP_FUSED || e.ta.p || e.cmul != 1.0f || e.cadd != 0.0f) return -1;
+  if (fp8) {
+    if (e.act != HKX_ACT_NONE) return -1;
+    if (!e.cs.p && !e.rs.p && !e.ra.p) return kEpNone;
+    if (!vec32_16(e.cs) || !vec32_16(e.rs)) return -1;
+    if (!e.ra.p) return kEpDeq;
+    return vec16_16(e.ra) ? kEpDeqBias : -1;
+  }
+  if (e.cs.p || e.rs.p) return -1;
+  if (!e.ra.p) return kEpNone;
+  return vec16_16(e.ra) ? kEpBias : -1;
 }
+
+}  // namespace
+
+bool quad_takes(const TileArgs& a, bool fp8, int mode) { return quad_form(a, fp8, mode) >= 0; }
 
 #define HKX_QUAD(ACT, EPF) hipLaunchKernelGGL((quad_kernel<ACT, EPF>), grid, dim3(512), 0, s, a)
 #define HKX_QUAD_ACTS(EPF)                                            \
@@ -27,15 +45,24 @@ bool quad_takes(const TileArgs& a, bool fp8, int mode) {
     default: HKX_QUAD(HKX_ACT_NONE, EPF); break;                    \
   }
 
-hipError_t launch_quad(const TileArgs& a, int mode, dim3 grid, hipStream_t s) {
-  if (!quad_takes(a, false, mode)) return hipErrorInvalidValue;
+hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s) {
+  const int epf = quad_form(a, fp8, mode);
+  if (epf < 0) return hipErrorInvalidValue;
+  if (fp8) {
+    if (epf == kEpDeqBias)
+      hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpDeqBias, false, true>), grid, dim3(512), 0, s, a);
+    else if (epf == kEpDeq)
+      hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpDeq, false, true>), grid, dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, false, true>), grid, dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   if (mode == kPair16) {
     hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, true>), grid, dim3(512), 0, s, a);
     return hipGetLastError();
   }
-  const bool fused = a.ep.form == HKX_EP_FUSED;
-  const int act = fused ? a.ep.act : HKX_ACT_NONE;
-  if (fused && a.ep.ra.p) { HKX_QUAD_ACTS(kEpBias) }
+  const int act = a.ep.form == HKX_EP_FUSED ? a.ep.act : HKX_ACT_NONE;
+  if (epf == kEpBias) { HKX_QUAD_ACTS(kEpBias) }
   else { HKX_QUAD_ACTS(kEpNone) }
   return hipGetLastError();
 }

@@ -41,18 +41,21 @@
 // past M by its buffer bound and predicated on n < N (N % 8 == 0).
 #pragma once
 
+#include <type_traits>
+
 #include "hkx_ring.hpp"
 
 namespace hkx {
 
-template <int ACT, int EPF, bool PAIR = false>
+template <int ACT, int EPF, bool PAIR = false, bool FP8 = false>
 __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   constexpr int BM = 256, BN = PAIR ? 128 : 256;  // BN: C columns of a tile
   constexpr int QB = 128 * 128;       // one quarter: 128 rows x 128 bytes
-  constexpr int BIAS = 8 * QB;        // then the bias: [tile % 3][1 KB]
-  constexpr int SMEM = BIAS + 3 * 1024;
-  static_assert(EPF == kEpNone || EPF == kEpBias, "forms");
-  static_assert(!PAIR || (EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
+  constexpr int EPV = 8 * QB;         // then the epilogue's vectors: [tile % 3][cs, rs, ra][1 KB]
+  constexpr int SMEM = EPV + 3 * 3 * 1024;
+  static_assert(FP8 ? (EPF == kEpNone || EPF == kEpDeq || EPF == kEpDeqBias) && ACT == HKX_ACT_NONE
+                    : (EPF == kEpNone || EPF == kEpBias), "forms");
+  static_assert(!PAIR || (!FP8 && EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
   static_assert(SMEM <= 160 * 1024, "LDS");
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
@@ -135,63 +138,91 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       buf_load16_lds(isb ? rb : ra, base + k * 1024, (isb ? lrow_b[k] : lrow[k]) * ld + lch[k], so);
   };
 
-  // ---- the bias of local tile lt: 256 bf16 by 16-byte DMA from wave 0 into slot lt % 3
-  // (lanes 32-63 read past the tile's 512 bytes into the slot's spare half). Three slots:
+  // ---- the epilogue's vectors of local tile lt by 16-byte DMA into slot lt % 3: the row
+  // scale (256 fp32, wave 0), the column scale (256 fp32, wave 1), the bias (256 bf16, wave
+  // 2; lanes 32-63 read past the tile's 512 bytes into the slot's spare half). Three slots:
   // the DMA of tile lt + 1, at tile lt's first phase, runs while group 1 may still read
   // tile lt - 1's.
-  constexpr bool bias = EPF == kEpBias;
-  const __amdgpu_buffer_rsrc_t rbias =
-      make_rsrc(bias ? p.ep.ra.p : nullptr, bias ? (uint32_t)p.N * 2u : 0u);
-  auto bias_load = [&](int lt) {
-    if (!bias || wave != 0) return;
+  constexpr bool bias = EPF == kEpBias || EPF == kEpDeqBias;
+  constexpr bool deq = EPF == kEpDeq || EPF == kEpDeqBias;
+  const Fused& e = p.ep;
+  const __amdgpu_buffer_rsrc_t rvec = make_rsrc(
+      wave == 0 ? (deq ? e.cs.p : nullptr) : wave == 1 ? (deq ? e.rs.p : nullptr) : (bias ? e.ra.p : nullptr),
+      wave == 0 ? (deq ? (uint32_t)p.M * 4u : 0u)
+                : wave == 1 ? (deq ? (uint32_t)p.N * 4u : 0u) : (bias ? (uint32_t)p.N * 2u : 0u));
+  auto vec_load = [&](int lt) {
+    if (wave > 2 || (wave < 2 && !deq) || (wave == 2 && !bias)) return;
     int m0, n0;
     tile_at(lt, m0, n0);
+    const uint32_t so = wave == 0 ? (uint32_t)m0 * 4u : wave == 1 ? (uint32_t)n0 * 4u : (uint32_t)n0 * 2u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rbias, (__attribute__((address_space(3))) void*)(smem + BIAS + (lt % 3) * 1024), 16,
-        (uint32_t)lane * 16u, __builtin_amdgcn_readfirstlane((uint32_t)n0 * 2u), 0, 0);
+        rvec, (__attribute__((address_space(3))) void*)(smem + EPV + (lt % 3) * 3072 + wave * 1024), 16,
+        (uint32_t)lane * 16u, __builtin_amdgcn_readfirstlane(so), 0, 0);
   };
 
-  // ---- fragment reads (16 x 16 x 32: lane l reads row l % 16 of a 16-row fragment,
-  // 16-byte chunk l / 16 of the K-half). A fragment of quarter rows r0.. (r0 % 16 == 0)
-  // at K-half s sits at r0 * 128 + s * 512 + rdo[(r0 >> 4) & 1].
+  // ---- fragment reads. bf16 (16 x 16 x 32): lane l reads row l % 16 of a 16-row
+  // fragment, 16-byte chunk l / 16 of the K-half; a fragment of quarter rows r0..
+  // (r0 % 16 == 0) at K-half s sits at r0 * 128 + s * 512 + rdo[(r0 >> 4) & 1]. fp8
+  // (32 x 32 x 64): lane l reads row l % 32 of a 32-row fragment, chunks h and 2 + h of the
+  // K-half (h = l / 32): the scaled MFMA takes a lane's bytes 0-15 as K block 0 of its 64
+  // and 16-31 as block 1, so lane half h holds K [16 h, +16) of each 32-K block; at
+  // r0 * 128 + s * 512 + rdo[0 or 1].
   uint32_t rdo[2];
-  {
+  if constexpr (FP8) {
+    const int rf = lane & 31, h = lane >> 5;
+    const int sw = ((rf >> 4) & 1) | (((rf >> 3) & 1) << 1);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      rdo[q] = (uint32_t)((rf >> 3) * 1024 + (rf & 7) * 64 + (((2 * q + h) ^ sw) << 4));
+  } else {
     const int rr = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int par = 0; par < 2; ++par)
       rdo[par] = (uint32_t)((rr >> 3) * 1024 + (rr & 7) * 64 + ((q ^ (par | ((rr >> 3) << 1))) << 4));
   }
-  bf16x8 af[4][2], bf0[2][2], bf1[2][2];  // [fragment][K-half]
+  constexpr int NA = FP8 ? 2 : 4, NB = FP8 ? 1 : 2;  // fragments of a block's A and B rows
+  using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
+  Frag af[NA][2], bf0[NB][2], bf1[NB][2];  // [fragment][K-half]
+  auto frag_at = [&](const uint8_t* s, int r0, int h, int par) -> Frag {
+    if constexpr (FP8) {
+      const i32x4 lo = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[0]);
+      const i32x4 hi = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[1]);
+      return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    } else {
+      return *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[par]);
+    }
+  };
   auto read_a = [&](int slot, int i) {
     const uint8_t* s = smem + (slot * 4 + i) * QB;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int r0 = grp * 64 + 16 * f;
+    for (int f = 0; f < NA; ++f)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) af[f][h] = *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[f & 1]);
-    }
+      for (int h = 0; h < 2; ++h) af[f][h] = frag_at(s, grp * 64 + (64 / NA) * f, h, f & 1);
   };
-  auto read_b = [&](int slot, int j, bf16x8 (&bf)[2][2]) {
+  auto read_b = [&](int slot, int j, Frag (&bf)[NB][2]) {
     const uint8_t* s = smem + (slot * 4 + 2 + j) * QB;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int r0 = wc * 32 + 16 * g;
+    for (int g = 0; g < NB; ++g)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) bf[g][h] = *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[g & 1]);
-    }
+      for (int h = 0; h < 2; ++h) bf[g][h] = frag_at(s, wc * 32 + 16 * g, h, g & 1);
   };
 
-  f32x4 acc[2][2][4][2];  // [A half][B half][row fragment][column fragment]
-  auto math = [&](int i, int j, const bf16x8 (&bf)[2][2], bool zero) {
+  using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
+  Acc acc[2][2][NA][NB];  // [A half][B half][row fragment][column fragment]
+  auto math = [&](int i, int j, const Frag (&bf)[NB][2], bool zero) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < NA; ++f)
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const f32x4 c = (zero && h == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j][f][g];
-          acc[i][j][f][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[g][h], af[f][h], c, 0, 0, 0);
+        for (int g = 0; g < NB; ++g) {
+          const Acc c = (zero && h == 0) ? Acc{} : acc[i][j][f][g];
+          if constexpr (FP8)
+            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
+                                                                              0, 0, 0);
+          else
+            acc[i][j][f][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[g][h], af[f][h], c, 0, 0, 0);
         }
     __builtin_amdgcn_s_setprio(0);
   };
@@ -205,10 +236,50 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   auto epilogue = [&](int lt) {
     int m0, n0;
     tile_at(lt, m0, n0);
+    const uint8_t* ev = smem + EPV + (lt % 3) * 3072;  // cs, rs, ra
+    if constexpr (FP8) {
+      // 32 x 32: lane l (row l % 32, half h = l / 32) holds columns 8 g + 4 h + [0, 4) in
+      // run g of a fragment's 16 values; runs 2 t and 2 t + 1 trade halves
+      // (v_permlane32_swap), so lane l stores columns 16 t + 8 h + [0, 8)
+      const int rf = lane & 31, h = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const int ml = 128 * i + 64 * grp + 32 * f + rf;
+            [[maybe_unused]] const float cs = deq ? ((const float*)ev)[ml] : 1.0f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              __builtin_amdgcn_sched_barrier(0);
+              const int c0 = 128 * j + 32 * wc + 16 * t;
+              f32x4 v[2];
+#pragma unroll
+              for (int u = 0; u < 2; ++u) {
+                const Acc& a = acc[i][j][f][0];
+                const int r = 8 * t + 4 * u;
+                v[u] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
+                const int col = c0 + 8 * u + 4 * h;
+                if constexpr (deq) v[u] = v[u] * (*(const f32x4*)(ev + 1024 + col * 4) * cs);
+                if constexpr (bias) v[u] += unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
+              }
+              const u32x2 w0 = pack4<2>(HKX_BF16, v[0]), w1 = pack4<2>(HKX_BF16, v[1]);
+              uint32_t x0 = w0.x, x1 = w1.x, y0 = w0.y, y1 = w1.y;
+              swap32(x0, x1);
+              swap32(y0, y1);
+              const int n = c0 + 8 * h;
+              if (n0 + n < p.N)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    i32x4{(int)x0, (int)y0, (int)x1, (int)y1}, rc,
+                    (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u, 0, 0);
+            }
+          }
+    } else {
     const int rf = lane & 15, q = lane >> 4;
     [[maybe_unused]] f32x4 bv[2][2];
     if constexpr (bias) {
-      const uint32_t* bs = (const uint32_t*)(smem + BIAS + (lt % 3) * 1024);
+      const uint32_t* bs = (const uint32_t*)(ev + 2048);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -263,6 +334,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                 (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u, 0, 0);
         }
       }
+    }
   };
 
   // ---- the K loop. Before the first phase: K-tile 0 whole and K-tile 1 but A1, in the
@@ -280,7 +352,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
-  bias_load(0);
+  vec_load(0);
   Stream s1 = stream_at(0), s2 = stream_at(0);
   fill(2, s2);
   fill(0, s2);
@@ -303,7 +375,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       // phase 1
       read_a(slot, 0);
       read_b(slot, 0, bf0);
-      if (t == 0 && lt + 1 < my_tiles) bias_load(lt + 1);
+      if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
       fill(1, s1);
       advance(s1);
       sync_mem();

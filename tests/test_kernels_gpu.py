@@ -464,3 +464,37 @@ def test_ring_quad(form, mnk, half):
         ref = O.silu(acc)
         _run(a.to(DEV), b.to(DEV), c, ep=_fused([], act=nat.ACT_SILU), **kw)
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["quad", "halfstage"])
+@pytest.mark.parametrize("form", ["plain", "deq", "deq_bias"])
+@pytest.mark.parametrize("mnk", [(256, 256, 128), (300, 520, 256), (4096, 4352, 384),
+                                 (1000, 2048, 1152), (2048, 9216, 512)])
+def test_ring_quad_fp8(form, mnk, half):
+    """fp8 e4m3 on the quadrant kernel (K-tiles of 128: a whole line) and, with
+    HKX_RING_HALFSTAGE, on the half-stage ring kernel: unscaled, per-token x per-channel
+    dequant, and dequant + bias; K-tile counts 1-9, ragged M and N, two tiles a workgroup,
+    wave split at 2048 x 9216."""
+    m, n, k = mnk
+    g = torch.Generator().manual_seed(70)
+    a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
+    sa = (torch.rand(m, 1, generator=g) + 0.5) / 448
+    sb = (torch.rand(n, generator=g) + 0.5) / 448
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    variant = (nat.RING_HALFSTAGE if half else 0) | (nat.RING_WAVESPLIT if n == 9216 else 0)
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, variant=variant)
+    c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
+    if form == "plain":
+        _run(a8.to(DEV), b8.to(DEV), c, **kw)
+        ref = O.gemm_fp32(a8.float(), b8.float())
+        O.assert_close(c, ref, rtol=1e-2, atol=1e-2 * ref.abs().max().item())
+        return
+    if form == "deq":
+        _run(a8.to(DEV), b8.to(DEV), c, ep=_fused([(sad, nat.COL), (sbd, nat.ROW)], cs=0, rs=1), **kw)
+        O.assert_close(c, O.scaled_mm(a8, b8, sa, sb), rtol=3e-2, atol=1e-2)
+        return
+    _run(a8.to(DEV), b8.to(DEV), c, ep=_fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)],
+                                              cs=0, rs=1, ra=2), **kw)
+    O.assert_close(c, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
