@@ -133,6 +133,14 @@ def test_workspace_sizes():
     assert L.hkx_gemm_workspace(ctypes.byref(sk)) == 0
     sk.variant = nat.RING_STREAMK | nat.RING_WAVESPLIT
     assert _check(sk)[0] == nat.ERR_ARG
+    # HKX_RING_HALFSTAGE combines with either; it is a ring-schedule bit only
+    for v in (nat.RING_HALFSTAGE, nat.RING_HALFSTAGE | nat.RING_WAVESPLIT,
+              nat.RING_HALFSTAGE | nat.RING_STREAMK):
+        sk.variant = v
+        assert _check(sk)[0] == nat.OK, v
+    pp = _args(m=2048, n=8192, k=512, tile_m=256, tile_n=256, tile_schedule=nat.TILE_PINGPONG,
+               variant=nat.RING_HALFSTAGE)
+    assert _check(pp)[0] == nat.ERR_ARG
 
 
 def test_mx_workspace_sizes():
