@@ -16,18 +16,17 @@
 //   32-63. One fill instruction moves one block: lanes l and l + 32 fetch the two halves
 //   of row l % 32 / 4's line, so every request is a whole line, and the 64-byte K-halves
 //   keep the bank pattern of 64-byte rows (16-byte chunk c of row r at c ^ swz4(r)).
-// * Phases. Per K-tile t, four phases, each: LDS reads into registers, one fill (the
-//   wave's 2 KB share of a quarter), a barrier, 16 MFMAs (v_mfma_f32_16x16x32_bf16), a
+// * Phases. Per K-tile t, two phases, each: LDS reads into registers, fills, a barrier,
+//   the MFMAs of two blocks (32 v_mfma_f32_16x16x32_bf16, or 8 fp8 32 x 32 x 64), a
 //   barrier:
-//     1: read A0(t) and B0(t); fill A1(t + 1);  math (0, 0)
-//     2: read B1(t);           fill B0(t + 2);  math (0, 1)
-//     3: read A1(t);           fill A0(t + 2);  math (1, 0)
-//     4:                       fill B1(t + 2);  math (1, 1)
+//     1: read A0(t), B0(t), B1(t); fill A1(t + 1);                 math (0, 0), (0, 1)
+//     2: read A1(t);               fill B0, B1, A0 of t + 2;       math (1, 0), (1, 1)
 //   A quarter is refilled only in a phase after both groups read it (group 1 runs one
 //   barrier behind group 0, so its reads of phase k land under group 0's MFMAs of phase
-//   k); each fill is 5-7 phases ahead of its first read. Before each barrier a wave waits
-//   for all but its 10 newest fill instructions: in issue order the five quarters after
-//   the one the next phase reads.
+//   k); each fill is about three phases ahead of its first read. Before each barrier a
+//   wave waits for all but its 8 newest fill instructions: in issue order the four
+//   quarters after the one the next phase reads. (Four phases of one block each, the
+//   reference's pp order, ran 3-7% slower: twice the barriers for the same MFMAs.)
 // * Tiles follow one another without a break in the fills (K-tile indices run on across
 //   the workgroup's tiles); the epilogue stores from the accumulators after the tile's
 //   last phase. A tile's bias reaches LDS by DMA during the tile before it (three slots
@@ -338,33 +337,33 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   };
 
   // ---- the K loop. Before the first phase: K-tile 0 whole and K-tile 1 but A1, in the
-  // order the steady state issues them (B0, A0, B1 of t + 2 in phases 2-4 of t, A1 of t + 1
+  // order the steady state issues them (B0, B1, A0 of t + 2 in phase 2 of t, A1 of t + 1
   // in phase 1 of t).
   auto sync_mem = [&]() {  // before a math phase: this wave's LDS reads landed
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(10));
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto sync_math = [&]() {  // before a memory phase: the quarter it reads landed everywhere
+  auto sync_math = [&]() {  // before a memory phase: the quarters it reads landed everywhere
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm(10));
+    __builtin_amdgcn_s_waitcnt(wait_vm(8));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
   vec_load(0);
   Stream s1 = stream_at(0), s2 = stream_at(0);
   fill(2, s2);
-  fill(0, s2);
   fill(3, s2);
+  fill(0, s2);
   fill(1, s1);
   advance(s1);
   advance(s2);
   fill(2, s2);
-  fill(0, s2);
   fill(3, s2);
+  fill(0, s2);
   advance(s2);
-  __builtin_amdgcn_s_waitcnt(wait_vm(10));  // A0 and B0 of K-tile 0
+  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // A0, B0 and B1 of K-tile 0
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();
   int g = 0;
@@ -375,28 +374,22 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       // phase 1
       read_a(slot, 0);
       read_b(slot, 0, bf0);
+      read_b(slot, 1, bf1);
       if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
       fill(1, s1);
       advance(s1);
       sync_mem();
       math(0, 0, bf0, z);
-      sync_math();
-      // phase 2
-      read_b(slot, 1, bf1);
-      fill(2, s2);
-      sync_mem();
       math(0, 1, bf1, z);
       sync_math();
-      // phase 3
+      // phase 2
       read_a(slot, 1);
-      fill(0, s2);
-      sync_mem();
-      math(1, 0, bf0, z);
-      sync_math();
-      // phase 4
+      fill(2, s2);
       fill(3, s2);
+      fill(0, s2);
       advance(s2);
       sync_mem();
+      math(1, 0, bf0, z);
       math(1, 1, bf1, z);
       sync_math();
     }
