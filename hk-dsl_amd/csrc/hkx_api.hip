@@ -666,6 +666,8 @@ int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const ui
   const hipStream_t s = (hipStream_t)stream;
   if (splits == 1) {
     const dim3 g(std::min(t.tiles_m * t.tiles_n, cu_count()));
+    // the quadrant kernel (whole-line fills) where it takes the call, else the ring's MX form
+    if (hkx::quad_takes(t, true, hkx::kStore16)) return launched(hkx::launch_quad_mx(t, g, s), "mx GEMM");
     return launched(hkx::launch_ring_mx(t, false, g, s), "mx GEMM");
   }
   const size_t need = hkx_mx_gemm_workspace(m, n, k);

@@ -43,6 +43,8 @@ hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 g
 // stride, 16-byte aligned; quad_takes says which calls.
 bool quad_takes(const TileArgs& a, bool fp8, int mode);
 hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
+// Its MX form (fp8 operands, E8M0 block scales in a.sa / a.sb, bf16 C, one pass).
+hipError_t launch_quad_mx(const TileArgs& a, dim3 grid, hipStream_t s);
 // The MX form (fp8 operands, E8M0 block scales in a.sa / a.sb), no epilogue: bf16 C, or
 // fp32 shares of a K split (f32_shares, a.c the workspace, grid.y the splits).
 hipError_t launch_ring_mx(const TileArgs& a, bool f32_shares, dim3 grid, hipStream_t s);

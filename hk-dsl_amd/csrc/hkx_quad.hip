@@ -67,4 +67,10 @@ hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStre
   return hipGetLastError();
 }
 
+hipError_t launch_quad_mx(const TileArgs& a, dim3 grid, hipStream_t s) {
+  if (quad_form(a, true, kStore16) != kEpNone || a.ep.form != HKX_EP_NONE) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, false, true, true>), grid, dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace hkx

@@ -46,12 +46,16 @@
 
 namespace hkx {
 
-template <int ACT, int EPF, bool PAIR = false, bool FP8 = false>
+template <int ACT, int EPF, bool PAIR = false, bool FP8 = false, bool MX = false>
 __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   constexpr int BM = 256, BN = PAIR ? 128 : 256;  // BN: C columns of a tile
   constexpr int QB = 128 * 128;       // one quarter: 128 rows x 128 bytes
   constexpr int EPV = 8 * QB;         // then the epilogue's vectors: [tile % 3][cs, rs, ra][1 KB]
-  constexpr int SMEM = EPV + 3 * 3 * 1024;
+  // MX: in their place, E8M0 scale chunks [chunk % 3][512 rows: A, then B][16 bytes]; a chunk
+  // the scales of 4 K-tiles (16 blocks of 32 K) of every row of the tile
+  constexpr int SCO = EPV;
+  constexpr int SMEM = EPV + (MX ? 3 * 8192 : 3 * 3 * 1024);
+  static_assert(!MX || (FP8 && EPF == kEpNone), "MX scales go with fp8 operands, no epilogue");
   static_assert(FP8 ? (EPF == kEpNone || EPF == kEpDeq || EPF == kEpDeqBias) && ACT == HKX_ACT_NONE
                     : (EPF == kEpNone || EPF == kEpBias), "forms");
   static_assert(!PAIR || (!FP8 && EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
@@ -137,6 +141,24 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       buf_load16_lds(isb ? rb : ra, base + k * 1024, (isb ? lrow_b[k] : lrow[k]) * ld + lch[k], so);
   };
 
+  // ---- MX scales: with the B0 fill of a chunk's first K-tile, wave w moves 16 bytes of each
+  // of rows 64 w + [0, 64) (A rows, then B) -- the chunk's 16 blocks -- into buffer
+  // (chunk) % 3. A chunk is read at its K-tiles' first phases; its buffer is refilled three
+  // chunks on, at the earliest a K-tile after its last read.
+  const int cpt = (nkt + 3) >> 2;  // chunks a tile
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(MX ? (wave < 4 ? p.sa : p.sb) : nullptr,
+                                               MX ? (wave < 4 ? p.sa_bytes : p.sb_bytes) : 0u);
+  auto scale_fill = [&](const Stream& st) {
+    if constexpr (MX) {
+      if (st.t & 3) return;
+      const int chunk = st.lt * cpt + (st.t >> 2);
+      const uint32_t row = (uint32_t)((wave < 4 ? st.m0 : st.n0) + 64 * (wave & 3) + lane);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsc, (__attribute__((address_space(3))) void*)(smem + SCO + (chunk % 3) * 8192 + wave * 1024), 16,
+          row * (wave < 4 ? p.sa_ld : p.sb_ld), __builtin_amdgcn_readfirstlane((uint32_t)st.t * 4u), 0, 0);
+    }
+  };
+
   // ---- the epilogue's vectors of local tile lt by 16-byte DMA into slot lt % 3: the row
   // scale (256 fp32, wave 0), the column scale (256 fp32, wave 1), the bias (256 bf16, wave
   // 2; lanes 32-63 read past the tile's 512 bytes into the slot's spare half). Three slots:
@@ -206,6 +228,23 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       for (int h = 0; h < 2; ++h) bf[g][h] = frag_at(s, wc * 32 + 16 * g, h, g & 1);
   };
 
+  // MX: the E8M0 dword of each of this lane's fragment rows for the K-tile (its 4 blocks,
+  // byte 2 s + h for K-half s and lane half h), read at the K-tile's first phase
+  [[maybe_unused]] uint32_t sca[2][2], scb[2];  // [A half][fragment], [B half]
+  auto read_scales = [&](int lt, int t) {
+    if constexpr (MX) {
+      const uint32_t* sc = (const uint32_t*)(smem + SCO + ((lt * cpt + (t >> 2)) % 3) * 8192) + (t & 3);
+      const int rf = lane & 31;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) sca[i][f] = sc[4 * (128 * i + 64 * grp + 32 * f + rf)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) scb[j] = sc[4 * (256 + 128 * j + 32 * wc + rf)];
+    }
+  };
+  const int sc_sh = 8 * (lane >> 5);
+
   using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
   Acc acc[2][2][NA][NB];  // [A half][B half][row fragment][column fragment]
   auto math = [&](int i, int j, const Frag (&bf)[NB][2], bool zero) {
@@ -217,7 +256,11 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
         for (int g = 0; g < NB; ++g) {
           const Acc c = (zero && h == 0) ? Acc{} : acc[i][j][f][g];
-          if constexpr (FP8)
+          if constexpr (MX)
+            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                bf[g][h], af[f][h], c, 0, 0, 0, (int)(scb[j] >> (16 * h + sc_sh)), 0,
+                (int)(sca[i][f] >> (16 * h + sc_sh)));
+          else if constexpr (FP8)
             acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
                                                                               0, 0, 0);
           else
@@ -354,12 +397,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   vec_load(0);
   Stream s1 = stream_at(0), s2 = stream_at(0);
   fill(2, s2);
+  scale_fill(s2);
   fill(3, s2);
   fill(0, s2);
   fill(1, s1);
   advance(s1);
   advance(s2);
   fill(2, s2);
+  scale_fill(s2);
   fill(3, s2);
   fill(0, s2);
   advance(s2);
@@ -375,6 +420,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       read_a(slot, 0);
       read_b(slot, 0, bf0);
       read_b(slot, 1, bf1);
+      read_scales(lt, t);
       if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
       fill(1, s1);
       advance(s1);
@@ -385,6 +431,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       // phase 2
       read_a(slot, 1);
       fill(2, s2);
+      scale_fill(s2);
       fill(3, s2);
       fill(0, s2);
       advance(s2);
