@@ -32,6 +32,10 @@
 //   last phase. A tile's bias reaches LDS by DMA during the tile before it (three slots
 //   by tile), so the epilogue's reads wait for no fill.
 //
+// The MX form (fp8 with E8M0 block scales, bf16 C): each K-tile's 4 scale bytes a row reach
+// LDS with the B0 fill of every 4th K-tile, 16 bytes a row, through three rotating buffers;
+// a lane passes its fragment row's byte for its 32-K block to the scaled MFMA.
+//
 // The paired form (C = silu(gate) * up, B's gate and up rows pair_off apart) reads 64 gate
 // and 64 up rows a B quarter, so a wave's two 16-row B fragments of a block are the gate
 // and up rows of the same 16 C columns; a tile is 128 C columns.

@@ -3,7 +3,8 @@
 The reference's contract (python/hk/ops/mxfp8.py:1-110): A (M, K) and B (N, K) fp8 e4m3,
 K-contiguous (F.linear's layout); sa (M, K/32) and sb (N, K/32) their E8M0 scales, one byte
 a row and 32 columns (the OCP MX layout; a 32 x 32-block weight scale is its rows repeated,
-`expand_block_scales`). Here the product runs on the ring GEMM kernel's MX form: every MFMA
+`expand_block_scales`). Here the product runs on the quadrant GEMM kernel's MX form (the
+ring kernel's where K is split over workgroups): every MFMA
 is gfx950's scaled one (v_mfma_scale_f32_32x32x64_f8f6f4), each lane passing the E8M0 byte
 of its own fragment row and 32-K block; the scales reach LDS by the same DMA as the
 operands, 16 bytes a row every 8 half-stages (whole lines: one 4-byte load a row and
