@@ -605,7 +605,7 @@ static int mx_splits(int32_t m, int32_t n, int32_t k) {
   if (m < 1 || n < 1 || k < 128 || k % 128) return 1;
   const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
   const int cu = cu_count();
-  if (2 * tiles > cu || (long long)m * n * 4 >= (1LL << 32)) return 1;
+  if (2 * tiles > cu || (long long)((m + 255) / 256) * 256 * n * 4 >= (1LL << 32)) return 1;
   const int s = std::min(std::min(cu / tiles, (k / 128) / 8), 8);
   if (s < 2) return 1;
   const int kper = (k / 128 + s - 1) / s;  // no empty last split
@@ -633,8 +633,10 @@ int hkx_mx_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, const ui
     return fail(HKX_ERR_SHAPE, "mx_gemm: C (bf16) needs 16-byte aligned rows");
   if (!aligned(sa, 4) || !aligned(sb, 4) || sa_ld % 4 || sb_ld % 4)
     return fail(HKX_ERR_SHAPE, "mx_gemm: the scales need 4-byte aligned rows");
+  // 32-bit byte offsets, C's computed for every row of the last 256-row tile (rows past M
+  // included, whose offsets must not wrap round into C's first rows)
   if ((long long)m * lda >= (1LL << 32) || (long long)n * ldb >= (1LL << 32) ||
-      (long long)m * ldc * 2 >= (1LL << 32))
+      (long long)((m + 255) / 256) * 256 * ldc * 2 >= (1LL << 32))
     return fail(HKX_ERR_SHAPE, "mx_gemm: A, B or C spans 4 GiB or more; split the call");
   hkx::TileArgs t{};
   t.a = a;

@@ -31,8 +31,10 @@ bool ring_takes(const TileArgs& a, bool fp8, int mode) {
   if (fp8 && (mode == kPair16 || mode == kPairWs)) return false;
   // whole 16-byte (8-byte for 8-bit C) pieces of rows
   if (ob != 4 && (a.N % 8 || !a.c_aligned || (a.ldc * ob) % 16)) return false;
-  // C (one split's share) is stored through a buffer resource: 32-bit byte offsets
-  if ((int64_t)a.M * a.ldc * ob >= (1LL << 32)) return false;
+  // C (one split's share) is stored through a buffer resource with 32-bit byte offsets,
+  // computed for every row of the last (ragged) 256-row tile, the rows past M included:
+  // those rows' offsets must not wrap round into C's first rows.
+  if ((int64_t)((a.M + 255) / 256) * 256 * a.ldc * ob >= (1LL << 32)) return false;
   // a 16-bit column scale is read as aligned pairs: unit stride only
   const Opnd& cs = a.ep.cs;
   if (a.ep.form == HKX_EP_FUSED && cs.p && cs.ld && cs.dt != HKX_FP32 && cs.ld != 1) return false;

@@ -375,8 +375,8 @@ def tune_linear(shapes: Dict[Tuple[int, int], str], ms: Sequence[int] = GRID, *,
             for path in ("hk", "hk_decode"):
                 if path == "hk_decode" and not gemm_cdna.fits("decode", m, n, k):
                     continue
-                run = vllm_gemm._run_for(path, m, n, k, False)
-                paths[path] = (lambda run: (lambda x, w, o: run(x, w, None, o)))(run)
+                run = vllm_gemm.launch_for(path, m, n, k, False)
+                paths[path] = (lambda run: (lambda x, w, o: run(x, w, None)))(run)
             us = bench.time(m, paths, rounds=rounds, log=log)
             pts.append([m, us])
             log(f"  {n}x{k} ({name}) M={m:5d}: {base_path(us, min_gain):9s} " +

@@ -1,20 +1,32 @@
-"""vLLM's unquantized linear layers on this build's gfx950 GEMMs.
+"""vLLM's unquantized linear layers on this build's gfx950 GEMMs, where a measured table
+says they are faster.
 
-Restates python/hk/integration/vllm_gemm.py's route (:1-693) over libhkx.so:
+The surface kept from the reference (python/hk/integration/vllm_gemm.py:1-693):
 
-* `torch.ops.hk_vllm.linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor`, an
-  opaque op with a fake, so under torch.compile the shape-dependent choice of kernel
-  is not a guard; it launches on torch's stream and declares itself graph-safe;
-* `route_for(m, n, k, ...)` -- "hk" (the tile / split-K kernels), "hk_decode" (the
-  decode kernel) or "fallback" (vLLM's own GEMM, or F.linear), from the measured
-  route table (`engine.RouteTable`): a shape nobody measured takes the fallback;
-* `dispatch_unquantized_gemm` rebound by identity in every vLLM module that imported it
-  (`apply` / `revert`), and each layer decided once (`decide_layers`).
+* the op `torch.ops.hk_vllm.linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor`,
+  y = x @ weight.T (+ bias) for x (..., K), weight (N, K); opaque to torch.compile (its
+  fake gives the output's shape), launched on torch's current stream, graph-safe;
+* `route_for(m, n, k, *, bf16, bias, contiguous_weight)` -> "hk" (the tile / split-K
+  GEMMs), "hk_decode" (the decode kernel) or "fallback" (vLLM's own GEMM, F.linear where
+  vLLM has none), read from hk/tuned/routes_vllm_linear_<arch>.json (`$HK_VLLM_ROUTES`
+  overrides it); a shape the table does not hold, or an M in a gap between two measured
+  runs, takes the fallback;
+* `apply()` rebinds vLLM's `dispatch_unquantized_gemm` in every vllm module that bound
+  it, and gives the patched engine a compile cache of its own; `revert()` puts it back;
+  `decide_layers(model)` decides every linear layer once, at load.
 
-One deliberate difference: a call with a bias can take the hk path, the bias added in
-the GEMM kernel's registers (the fused epilogue), where the reference sends it to the
-fallback (:173) rather than pay a second pass over the output. `BIAS_FUSED = False`
-restores the reference's behaviour.
+How it is put together here. `Router` owns the table and a memo of per-call-signature
+`Plan`s (path plus a launch); replacing the table starts a new generation, which drops
+the memo and invalidates the decision kept on each layer. A layer is decided from its
+weight alone -- whether the table routes its (N, K) at any M -- and a layer it never
+routes keeps vLLM's GEMM with no wrapper in its path. Nothing here writes state while
+torch.compile traces (vLLM compiles the forward whole and refuses a graph that replays
+a write): the dispatch stand-in keeps no cache, and a layer decision made while
+tracing is used, not stored.
+
+One difference from the reference: a call with a bias can take the hk paths, the bias
+added in the GEMM's registers (the fused epilogue); the reference sends bias calls to the
+fallback (:173). `BIAS_FUSED = False` restores that.
 """
 
 from __future__ import annotations
@@ -22,307 +34,371 @@ from __future__ import annotations
 import functools
 import sys
 from collections import Counter
-from typing import Any, Callable, Dict, Optional
+from typing import Callable, Dict, NamedTuple, Optional
 
 from . import engine
 
+#: Modules whose bindings of vLLM's dispatch function `apply` replaces.
 PREFIXES = ("vllm",)
 ROUTES_ENV = "HK_VLLM_ROUTES"
-#: Whether a bias rides the hk path as a fused epilogue (True) or falls back.
+#: Whether a bias rides the hk paths as a fused epilogue (True) or falls back.
 BIAS_FUSED = True
-
-_ORIG_DISPATCH: Optional[Callable] = None
-UNROUTED: "Counter[str]" = Counter()
-_GEMMS: Dict[Any, Callable] = {}
-_FALLBACK: list = []
-_TABLE: list = []
-_GEN = [0]
+#: What a table's runs may name.
+RUN_PATHS = ("hk", "hk_decode", "fallback")
+#: Signatures memoised before deciding afresh on every call (a serving engine's prefill
+#: has a new M per batch; the memo is a cache, not a record).
+PLAN_CAP = 4096
 
 
-def _linear_fake(x, weight, bias=None):
+def _fake(x, weight, bias=None):
     return x.new_empty((*x.shape[:-1], weight.shape[0]))
 
 
-RUN_PATHS = ("hk", "hk_decode", "fallback")
-
-PATCH = engine.Op("hk_vllm::linear", "linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor",
-                  _linear_fake, paths=RUN_PATHS, graph="safe")
+PATCH = engine.Op("hk_vllm::linear",
+                  "linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor",
+                  _fake, paths=RUN_PATHS, graph="safe")
+#: Calls by path (eager); `PATCH.captured` counts calls made while capturing a graph.
 STATS = PATCH.stats
+#: Layers left on vLLM's GEMM when decided, by reason.
+UNROUTED: "Counter[str]" = Counter()
+
+
+class Plan(NamedTuple):
+    path: str
+    run: Optional[Callable]     # (x2 (M, K), weight, bias) -> y (M, N)
+
+
+_FALLBACK_PLAN = Plan("fallback", None)
+
+
+class Router:
+    """The table in force and what was decided from it."""
+
+    def __init__(self):
+        self._table: Optional[engine.RouteTable] = None
+        self._loaded = False
+        self.generation = 0
+        self.plans: Dict[tuple, Plan] = {}
+
+    def table(self) -> Optional[engine.RouteTable]:
+        if not self._loaded:
+            from ..target import current_arch  # noqa: PLC0415
+
+            self._table = engine.shipped_table("vllm_linear", current_arch(), ROUTES_ENV)
+            self._loaded = True
+        return self._table
+
+    def replace(self, table: Optional[engine.RouteTable], *, loaded: bool) -> None:
+        self._table, self._loaded = table, loaded
+        self.plans.clear()
+        self.generation += 1
+
+
+ROUTER = Router()
 
 
 def routes() -> Optional[engine.RouteTable]:
-    """The routing table for this process's arch (loaded once; `set_routes(None)`
-    reloads it)."""
-    if not _TABLE:
-        from ..target import current_arch  # noqa: PLC0415
-
-        _TABLE.append(engine.shipped_table("vllm_linear", current_arch(), ROUTES_ENV))
-    return _TABLE[0]
+    """The routing table for this process's arch, loaded on first use, or None."""
+    return ROUTER.table()
 
 
 def set_routes(table: Optional[engine.RouteTable]) -> None:
-    """Route by `table` from now on; None for the shipped one."""
+    """Route by `table` from now on; None reloads the shipped one on next use. Graphs
+    captured before keep the launches they captured."""
     if any(PATCH.captured.values()):
         import warnings  # noqa: PLC0415
 
-        warnings.warn("hk_vllm::linear: routes changed after a CUDA graph was captured; graphs "
-                      "captured before keep replaying the old routes", stacklevel=2)
-    _TABLE.clear()
-    _PLANS.clear()
-    _GEN[0] += 1
-    if table is not None:
-        _TABLE.append(table)
+        warnings.warn("hk_vllm::linear: the routes changed after a CUDA graph captured calls "
+                      "of the op; those graphs replay the launches of the old routes",
+                      stacklevel=2)
+    ROUTER.replace(table, loaded=table is not None)
 
 
-def _gemm_takes(n: int, k: int) -> bool:
+# ---------------------------------------------------------------- deciding a call
+
+
+def _hk_takes(path: str, m: int, n: int, k: int) -> bool:
+    """Whether the kernel behind `path` takes an M x N x K call at all."""
     from ..ops import gemm_cdna  # noqa: PLC0415
 
-    return not (n % gemm_cdna.BLOCK_N_MIN or k % gemm_cdna.K_STEP)
+    if path == "hk":
+        return n % gemm_cdna.BLOCK_N_MIN == 0 and k % gemm_cdna.K_STEP == 0
+    if path == "hk_decode":
+        return gemm_cdna.fits("decode", m, n, k)
+    return False
 
 
 def route_for(m: int, n: int, k: int, *, bf16: bool = True, bias: bool = False,
               contiguous_weight: bool = True) -> str:
-    """"hk", "hk_decode" or "fallback" for y = x @ W.T (+ bias), x (m, k), W (n, k)."""
-    if m < 1 or not bf16 or not contiguous_weight or (bias and not BIAS_FUSED):
+    """Where y = x @ W.T (+ bias), x (m, k), W (n, k), goes: "hk", "hk_decode" or
+    "fallback". The table names the fastest measured path; it is taken only if its kernel
+    takes the call."""
+    if m < 1 or not bf16 or not contiguous_weight:
+        return "fallback"
+    if bias and not BIAS_FUSED:
         return "fallback"
     table = routes()
     if table is None:
         return "fallback"
     path = table.lookup(m, n, k)
-    if path == "hk" and not _gemm_takes(n, k):
+    if path not in ("hk", "hk_decode") or not _hk_takes(path, m, n, k):
         return "fallback"
-    if path == "hk_decode":
-        from ..ops import gemm_cdna  # noqa: PLC0415
-
-        if not gemm_cdna.fits("decode", m, n, k):
-            return "fallback"
-    return path if path in RUN_PATHS else "fallback"
+    return path
 
 
 def route(m: int, n: int, k: int, **how) -> bool:
+    """Whether the call goes to the tile GEMMs."""
     return route_for(m, n, k, **how) == "hk"
 
 
 def route_decode(m: int, n: int, k: int, **how) -> bool:
+    """Whether the call goes to the decode kernel."""
     return route_for(m, n, k, **how) == "hk_decode"
 
 
+def _schedule(path: str, m: int, n: int, k: int) -> str:
+    """The template's schedule for a routed path: the decode kernel for "hk_decode"; for
+    "hk" the GEMM route's tile candidate, or -- where that route would pick the decode
+    kernel, which the table measured as another path -- the tile rule's choice."""
+    from ..ops import gemm_cdna  # noqa: PLC0415
+
+    if path == "hk_decode":
+        return "decode"
+    name = gemm_cdna.route(m, n, k)
+    if gemm_cdna.CANDIDATES[name]["kernel"] != "tile":
+        name = gemm_cdna.rule(max(m, 33), n, k)      # the rule's tiles start at M = 33
+    return name
+
+
+def launch_for(path: str, m: int, n: int, k: int, has_bias: bool) -> Callable:
+    """The launch of a routed path: (x2, weight, bias) -> y, y allocated by the template
+    on the caller's stream."""
+    from ..templates import gemm as T  # noqa: PLC0415
+
+    sched = _schedule(path, m, n, k)
+    if has_bias:
+        return functools.partial(_with_bias, T.gemm, sched)
+    return functools.partial(_plain, T.gemm, sched)
+
+
+def _plain(gemm, sched, x2, weight, bias):
+    return gemm(x2, weight, schedule=sched)
+
+
+def _with_bias(gemm, sched, x2, weight, bias):
+    return gemm(x2, weight, epilogue=gemm.bias, schedule=sched, bias=bias)
+
+
+def _weight_ok(weight) -> bool:
+    """A weight the kernels read in place: contiguous (N, K), 16-byte aligned."""
+    return weight.dim() == 2 and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+
+
+def _decide(x, weight, bias, m: int, n: int, k: int) -> Plan:
+    import torch  # noqa: PLC0415
+
+    bf16 = x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != n or bias.dtype not in (
+            torch.bfloat16, torch.float16, torch.float32)):
+        return _FALLBACK_PLAN
+    path = route_for(m, n, k, bf16=bf16, bias=bias is not None,
+                     contiguous_weight=_weight_ok(weight))
+    if path == "fallback":
+        return _FALLBACK_PLAN
+    return Plan(path, launch_for(path, m, n, k, bias is not None))
+
+
+_ENGINE_GEMM: list = []
+
+
 def _fallback(x, weight, bias):
-    """What vLLM would have run: its own op where it has one, else F.linear."""
-    if not _FALLBACK:
+    """The engine's own GEMM: vLLM's ROCm op where vLLM registered one, else F.linear."""
+    if not _ENGINE_GEMM:
         import torch  # noqa: PLC0415
 
         try:
-            _FALLBACK.append(torch.ops.vllm.rocm_unquantized_gemm)
+            fn = torch.ops.vllm.rocm_unquantized_gemm
         except (AttributeError, RuntimeError):
-            _FALLBACK.append(torch.nn.functional.linear)
-    return _FALLBACK[0](x, weight, bias)
-
-
-#: (M, N, K, dtypes, bias, contiguity, device) -> (path, run), decided once per shape.
-_PLANS: Dict[tuple, tuple] = {}
-_PLAN_CAP = 4096
-
-
-def _run_for(path: str, m: int, n: int, k: int, has_bias: bool) -> Callable:
-    from ..ops import gemm_cdna  # noqa: PLC0415
-    from ..templates import gemm as T  # noqa: PLC0415
-
-    schedule = None
-    if path == "hk_decode":
-        schedule = "decode"
-    elif path == "hk":
-        name = gemm_cdna.route(m, n, k)
-        schedule = name if gemm_cdna.CANDIDATES[name]["kernel"] == "tile" else gemm_cdna.rule(
-            max(m, 33), n, k)
-    if has_bias:
-        return lambda x2, w, b, out: T.gemm(x2, w, epilogue=T.bias, out=out, schedule=schedule,
-                                            bias=b)
-    return lambda x2, w, b, out: T.gemm(x2, w, out=out, schedule=schedule)
-
-
-def _plan(x, weight, bias, m: int, n: int, k: int) -> tuple:
-    import torch  # noqa: PLC0415
-
-    path = route_for(m, n, k, bf16=x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16,
-                     bias=bias is not None, contiguous_weight=weight.is_contiguous())
-    if path == "fallback":
-        return "fallback", None
-    return path, _run_for(path, m, n, k, bias is not None)
+            fn = torch.nn.functional.linear
+        _ENGINE_GEMM.append(fn)
+    return _ENGINE_GEMM[0](x, weight, bias)
 
 
 def linear(x, weight, bias=None):
-    """y = x @ weight.T (+ bias), on the kernel the table names (vllm_gemm.py:384-416)."""
-    import torch  # noqa: PLC0415
-
+    """y = x @ weight.T (+ bias), on the path the table names (the op's body; reference
+    python/hk/integration/vllm_gemm.py:384-416)."""
     k = x.shape[-1]
-    m = x.numel() // k if k else 0
     n = weight.shape[0]
-    key = (m, n, k, x.dtype, weight.dtype, bias is None, weight.is_contiguous(), x.get_device())
-    plan = _PLANS.get(key)
+    m = x.numel() // k if k else 0
+    key = (m, n, k, x.dtype, weight.dtype, None if bias is None else bias.dtype,
+           _weight_ok(weight), x.get_device())
+    plan = ROUTER.plans.get(key)
     if plan is None:
-        plan = _plan(x, weight, bias, m, n, k)
-        if len(_PLANS) < _PLAN_CAP:
-            _PLANS[key] = plan
-    path, run = plan
-    if path == "fallback":
+        plan = _decide(x, weight, bias, m, n, k)
+        if len(ROUTER.plans) < PLAN_CAP:
+            ROUTER.plans[key] = plan
+    if plan.run is None:
         PATCH.count("fallback")
         return _fallback(x, weight, bias)
     x2 = x.reshape(m, k)
-    if not x2.is_contiguous():
-        x2 = x2.contiguous()
-    out = torch.empty((m, n), device=x.device, dtype=x.dtype)
-    run(x2, weight, bias, out)
-    PATCH.count(path)
-    return out.view(*x.shape[:-1], n)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.clone(memory_format=_contiguous())
+    y = plan.run(x2, weight, bias)
+    PATCH.count(plan.path)
+    return y.view(*x.shape[:-1], n)
 
 
-def register_op():
-    """Define `torch.ops.hk_vllm.linear`. Idempotent."""
+def _contiguous():
+    import torch  # noqa: PLC0415
+
+    return torch.contiguous_format
+
+
+def register_op() -> None:
+    """Define `torch.ops.hk_vllm.linear` (idempotent)."""
     PATCH.define(linear)
 
 
-def _unrouted(weight, bias) -> str:
-    """Why the table takes no call of a layer with this weight, at any M ("" if some)."""
+# ---------------------------------------------------------------- layers and vLLM
+
+
+def _unrouted_reason(weight, bias) -> str:
+    """Why no call of a layer with this weight and bias can take an hk path ("" if one
+    can)."""
     import torch  # noqa: PLC0415
 
     if weight.dtype != torch.bfloat16:
-        return f"weight {str(weight.dtype).replace('torch.', '')}"
+        return "weight " + str(weight.dtype).rpartition(".")[2]
     if bias is not None and not BIAS_FUSED:
         return "bias"
     if weight.dim() != 2 or not weight.is_contiguous():
         return "weight not a contiguous matrix"
     table = routes()
-    n, k = weight.shape
-    if table is None or not table.routes_any(n, k):
+    if table is None or not table.routes_any(*weight.shape):
         return "no route at any M"
     return ""
 
 
-def _compiling() -> bool:
-    import torch  # noqa: PLC0415
-
-    return torch.compiler.is_compiling()
-
-
-def _takes_layer(layer, weight, bias) -> bool:
-    """Whether this layer's calls go through the op at all, decided once per table
-    generation and kept on the layer (read-only while torch.compile traces)."""
-    memo = getattr(layer, "_hk_gemm", None)
-    if memo is not None and memo[0] == _GEN[0]:
-        return memo[1]
-    why = _unrouted(weight, bias)
-    if _compiling():
-        return not why
-    if why and (memo is None or memo[1]):
-        UNROUTED[why] += 1
+def _layer_routed(layer, weight, bias) -> bool:
+    """Whether a layer's calls go through the op. The decision is kept on the layer
+    (`_hk_route` = (generation, reason)) and reused until the table is replaced -- except
+    while torch.compile traces, where it is made and not kept."""
+    kept = getattr(layer, "_hk_route", None)
+    gen = ROUTER.generation
+    if kept is not None and kept[0] == gen:
+        return not kept[1]
+    reason = _unrouted_reason(weight, bias)
+    if engine.compiling():
+        return not reason
+    if reason and (kept is None or not kept[1]):
+        UNROUTED[reason] += 1
     try:
-        layer._hk_gemm = (_GEN[0], not why)
-    except AttributeError:
+        layer._hk_route = (gen, reason)
+    except AttributeError:      # a layer that takes no attributes is decided every call
         pass
-    return not why
+    return not reason
 
 
-def _gemm(layer, x, weight, bias=None):
-    import torch  # noqa: PLC0415
-
+def _layer_gemm(engine_gemm, layer, x, weight, bias=None):
+    """The GEMM a patched `dispatch_unquantized_gemm()` hands a layer: the op for a routed
+    layer's GPU calls, else what vLLM's own dispatch returned (`engine_gemm`)."""
+    if not _layer_routed(layer, weight, bias):
+        return engine_gemm(layer, x, weight, bias)
     if not x.is_cuda:
+        import torch  # noqa: PLC0415
+
         return torch.nn.functional.linear(x, weight, bias)
     return PATCH(x, weight, bias)
 
 
-def _routed_gemm(orig, layer, x, weight, bias=None):
-    if not _takes_layer(layer, weight, bias):
-        return orig(layer, x, weight, bias)
-    return _gemm(layer, x, weight, bias)
+_VLLM_DISPATCH: Optional[Callable] = None
 
 
 def dispatch_unquantized_gemm(*args, **kwargs):
-    """Stands in for vLLM's: returns the routed GEMM bound to vLLM's own (kept for the
-    layers the table never routes). Writes its cache only in eager code."""
-    try:
-        key = (args, tuple(sorted(kwargs.items())))
-        hit = _GEMMS.get(key)
-    except TypeError:
-        key, hit = None, None
-    if hit is not None:
-        return hit
-    g = functools.partial(_routed_gemm, _ORIG_DISPATCH(*args, **kwargs))
-    if key is not None and not _compiling():
-        _GEMMS[key] = g
-    return g
+    """Stands in for vLLM's: asks vLLM's own dispatch (its arguments pick among backends,
+    which is vLLM's business) and binds what it returns as the layer's fallback. vLLM
+    calls this on every forward, inside the graph it compiles, so it keeps no cache."""
+    return functools.partial(_layer_gemm, _VLLM_DISPATCH(*args, **kwargs))
 
 
 def rebind(prefixes, old, new) -> list:
-    """Replace every module-level binding of `old` by `new` in the modules whose name
-    starts with one of `prefixes`, by identity. Returns the names rebound."""
-    names = []
-    for modname, mod in list(sys.modules.items()):
-        if mod is None or not modname.startswith(tuple(prefixes)):
+    """Point every module-level name bound to `old` at `new`, in the loaded modules whose
+    name starts with one of `prefixes`; returns "module.name" of each."""
+    done = []
+    for modname in sorted(sys.modules):
+        if not modname.startswith(tuple(prefixes)):
+            continue
+        mod = sys.modules.get(modname)
+        if mod is None:
             continue
         for attr, val in list(vars(mod).items()):
             if val is old:
                 setattr(mod, attr, new)
-                names.append(f"{modname}.{attr}")
-    return names
+                done.append(f"{modname}.{attr}")
+    return done
 
 
 def apply() -> str:
-    """Route vLLM's linear layers. Returns what happened, in one line."""
-    global _ORIG_DISPATCH
+    """Route vLLM's unquantized linear layers. Returns what happened, in one line."""
+    global _VLLM_DISPATCH
+    if _VLLM_DISPATCH is not None:
+        return "linear: already patched"
     try:
-        from vllm.model_executor.layers import utils as vu  # noqa: PLC0415
+        from vllm.model_executor.layers import utils as vllm_utils  # noqa: PLC0415
         from vllm.platforms import current_platform  # noqa: PLC0415
     except ImportError:
         return "vllm is not importable; linear not patched"
-    if _ORIG_DISPATCH is not None:
-        return "linear: already patched"
     if not current_platform.is_rocm():
         return "linear: not patched -- not a ROCm platform"
     table = routes()
     if table is None:
         from ..target import current_arch  # noqa: PLC0415
 
-        return (f"linear: not patched -- no routing table for {current_arch()}; "
-                f"`python -m hk.integration.tune` measures one")
+        return (f"linear: not patched -- no routing table for {current_arch()} "
+                f"(`python -m hk.integration.tune` measures one)")
     register_op()
-    _GEMMS.clear()
-    _ORIG_DISPATCH = vu.dispatch_unquantized_gemm
-    names = rebind(PREFIXES, _ORIG_DISPATCH, dispatch_unquantized_gemm)
-    return f"linear -> hk where {table.source or 'the table'} measured it faster ({len(names)} rebound)"
+    _VLLM_DISPATCH = vllm_utils.dispatch_unquantized_gemm
+    names = rebind(PREFIXES, _VLLM_DISPATCH, dispatch_unquantized_gemm)
+    cache = engine.isolate_compile_cache("linear")
+    return (f"linear -> hk where {table.source or 'the table'} measured it faster "
+            f"({len(names)} rebound; compile cache {cache})")
 
 
 def revert() -> str:
-    global _ORIG_DISPATCH
-    if _ORIG_DISPATCH is None:
+    global _VLLM_DISPATCH
+    if _VLLM_DISPATCH is None:
         return "linear: not patched"
-    names = rebind(PREFIXES, dispatch_unquantized_gemm, _ORIG_DISPATCH)
-    _ORIG_DISPATCH = None
-    _GEMMS.clear()
+    names = rebind(PREFIXES, dispatch_unquantized_gemm, _VLLM_DISPATCH)
+    _VLLM_DISPATCH = None
     return f"linear -> vllm ({len(names)} rebound)"
 
 
+def _linear_layer_bias(mod, head):
+    """(is a GEMM layer, its bias) for a vLLM module: an unquantized linear (its bias
+    unless vLLM adds it afterwards) or the LM head (an embedding matrix used as a GEMM)."""
+    method = type(getattr(mod, "quant_method", None)).__name__
+    if method == "UnquantizedLinearMethod":
+        return True, (None if getattr(mod, "skip_bias_add", False) else getattr(mod, "bias", None))
+    if method == "UnquantizedEmbeddingMethod":
+        return (mod is head or type(mod).__name__ == "ParallelLMHead"), None
+    return False, None
+
+
 def decide_layers(model) -> str:
-    """Decide every unquantized linear layer of a loaded vLLM model (and its LM head) now."""
+    """Decide every unquantized linear layer of a loaded vLLM model and its LM head now,
+    before vLLM's profile run or any capture. Returns the report line."""
     import torch  # noqa: PLC0415
 
     head = getattr(model, "lm_head", None)
     routed = 0
-    for _, mod in model.named_modules():
+    for mod in model.modules():
         w = getattr(mod, "weight", None)
-        qm = type(getattr(mod, "quant_method", None)).__name__
         if not isinstance(w, torch.Tensor) or w.dim() != 2:
             continue
-        if qm == "UnquantizedEmbeddingMethod":
-            if mod is not head and type(mod).__name__ != "ParallelLMHead":
-                continue
-            bias = None
-        elif qm == "UnquantizedLinearMethod":
-            bias = None if getattr(mod, "skip_bias_add", False) else getattr(mod, "bias", None)
-        else:
-            continue
-        routed += _takes_layer(mod, w, bias)
-    return f"{routed} layer{'s' * (routed != 1)} through hk's op; {unrouted_status()}"
+        is_gemm, bias = _linear_layer_bias(mod, head)
+        if is_gemm:
+            routed += _layer_routed(mod, w, bias)
+    return f"{routed} layer{'' if routed == 1 else 's'} through hk's op; {unrouted_status()}"
 
 
 def unrouted_status() -> str:
@@ -332,9 +408,9 @@ def unrouted_status() -> str:
 
 
 def status() -> str:
-    return "not patched" if _ORIG_DISPATCH is None else f"patched; {unrouted_status()}"
+    return "not patched" if _VLLM_DISPATCH is None else f"patched; {unrouted_status()}"
 
 
-__all__ = ["PATCH", "STATS", "route_for", "route", "route_decode", "linear", "register_op",
-           "dispatch_unquantized_gemm", "apply", "revert", "decide_layers", "routes",
-           "set_routes", "rebind"]
+__all__ = ["PATCH", "STATS", "ROUTER", "route_for", "route", "route_decode", "linear",
+           "launch_for", "register_op", "dispatch_unquantized_gemm", "apply", "revert",
+           "decide_layers", "routes", "set_routes", "rebind", "status"]

@@ -23,12 +23,9 @@ shapes it measured, :33-56). Without a table, M >= MIN_M, the reference's measur
 
 from __future__ import annotations
 
-from typing import Callable, Optional
+from typing import Callable, Dict, Optional
 
 from . import engine
-
-_ORIG_PWAL: Optional[Callable] = None
-_ORIG_APPLY: Optional[Callable] = None
 
 #: The smallest M routed to hk.
 MIN_M = 2048
@@ -75,19 +72,22 @@ def schedule(m: int, n: int, k: int) -> bool:
     return t.lookup(m, n, k) == "hk"
 
 
-_VLLM: list = []
+class _VllmKernel:
+    """vLLM's own quant and GEMM for MXFP8 linears, imported on first use."""
 
+    quantize: Optional[Callable] = None
+    gemm: Optional[Callable] = None
 
-def _vllm_path():
-    """(mxfp8_e4m3_quantize, rocm_mxfp8_block32_gemm): vLLM's own quant and kernel."""
-    if not _VLLM:
-        from vllm.model_executor.kernels.linear.mxfp8.rocm_block32_gemm import (  # noqa: PLC0415
-            rocm_mxfp8_block32_gemm)
-        from vllm.model_executor.layers.quantization.utils.mxfp8_utils import (  # noqa: PLC0415
-            mxfp8_e4m3_quantize)
+    @classmethod
+    def load(cls):
+        if cls.gemm is None:
+            from vllm.model_executor.kernels.linear.mxfp8.rocm_block32_gemm import (  # noqa: PLC0415
+                rocm_mxfp8_block32_gemm)
+            from vllm.model_executor.layers.quantization.utils.mxfp8_utils import (  # noqa: PLC0415
+                mxfp8_e4m3_quantize)
 
-        _VLLM.extend((mxfp8_e4m3_quantize, rocm_mxfp8_block32_gemm))
-    return _VLLM
+            cls.quantize, cls.gemm = mxfp8_e4m3_quantize, rocm_mxfp8_block32_gemm
+        return cls
 
 
 def mxfp8_linear(x, w, ws, hk_ws, out_dtype):
@@ -98,84 +98,108 @@ def mxfp8_linear(x, w, ws, hk_ws, out_dtype):
     from ..ops import mxfp8  # noqa: PLC0415
 
     m, k = x.shape
-    n = w.shape[0]
-    if out_dtype == torch.bfloat16 and hk_ws.numel() and schedule(m, n, k):
+    if out_dtype == torch.bfloat16 and hk_ws.numel() and schedule(m, w.shape[0], k):
         PATCH.count("hk")
         return mxfp8.linear(x, w, hk_ws)
     PATCH.count("fallback")
-    quantize, gemm = _vllm_path()
-    xq, xs = quantize(x)
-    return gemm(xq, xs, w, ws, out_dtype)
+    v = _VllmKernel.load()
+    xq, xs = v.quantize(x)
+    return v.gemm(xq, xs, w, ws, out_dtype)
 
 
-def process_weights_after_loading(self, layer) -> None:
-    """vLLM's, then the weight's block scales one row each, beside vLLM's."""
-    import torch  # noqa: PLC0415
-
-    from ..ops import mxfp8  # noqa: PLC0415
-
-    _ORIG_PWAL(self, layer)
-    w, ws = layer.weight, layer.weight_scale
-    n, k = w.shape
-    if ws.shape[0] == n or w.element_size() != 1 or n % 8 or k % 128:
-        return  # not the block-scaled path, or a shape the kernel does not take
-    rows = mxfp8.expand_block_scales(ws.data.view(torch.uint8))[:n]
-    layer.hk_ws = torch.nn.Parameter(rows, requires_grad=False)
-
-
-def apply_weights(self, layer, x, bias=None):
-    if not hasattr(layer, "hk_ws"):
-        return _ORIG_APPLY(self, layer, x, bias)
-    x2d = x.reshape(-1, x.shape[-1])
-    out = PATCH(x2d, layer.weight, layer.weight_scale, layer.hk_ws, x.dtype)
-    out = out.reshape(*x.shape[:-1], layer.weight.shape[0])
-    if bias is not None:
-        out = out + bias
-    return out
-
-
-def _cls():
+def _kernel_class():
     from vllm.model_executor.kernels.linear.mxfp8 import rocm_native  # noqa: PLC0415
 
     return rocm_native.RocmDotScaledMxfp8LinearKernel
 
 
+class _MethodSwap:
+    """Methods of one class replaced by ours, with the originals kept to call through and
+    to put back."""
+
+    def __init__(self):
+        self.cls = None
+        self.orig: Dict[str, Callable] = {}
+
+    @property
+    def active(self) -> bool:
+        return self.cls is not None
+
+    def install(self, cls, ours: Dict[str, Callable]) -> None:
+        self.cls = cls
+        self.orig = {name: cls.__dict__[name] if name in cls.__dict__ else getattr(cls, name)
+                     for name in ours}
+        for name, fn in ours.items():
+            setattr(cls, name, fn)
+
+    def restore(self) -> None:
+        for name, fn in self.orig.items():
+            setattr(self.cls, name, fn)
+        self.cls, self.orig = None, {}
+
+
+SWAP = _MethodSwap()
+
+
+def process_weights_after_loading(self, layer) -> None:
+    """vLLM's, then the weight's block scales one row each (the OCP layout this build's
+    kernel reads), kept beside vLLM's as `layer.hk_ws`."""
+    import torch  # noqa: PLC0415
+
+    from ..ops import mxfp8  # noqa: PLC0415
+
+    SWAP.orig["process_weights_after_loading"](self, layer)
+    w, ws = layer.weight, layer.weight_scale
+    n, k = w.shape
+    block_scaled = ws.shape[0] != n and w.element_size() == 1
+    if not block_scaled or n % 8 or k % 128:
+        return
+    rows = mxfp8.expand_block_scales(ws.data.view(torch.uint8))[:n]
+    layer.hk_ws = torch.nn.Parameter(rows, requires_grad=False)
+
+
+def apply_weights(self, layer, x, bias=None):
+    """One call of the op for a layer with hk's scales; vLLM's for any other layer."""
+    if not hasattr(layer, "hk_ws"):
+        return SWAP.orig["apply_weights"](self, layer, x, bias)
+    n = layer.weight.shape[0]
+    y = PATCH(x.reshape(-1, x.shape[-1]), layer.weight, layer.weight_scale, layer.hk_ws,
+              x.dtype).reshape(*x.shape[:-1], n)
+    return y if bias is None else y + bias
+
+
 def apply_patch() -> str:
     """Route vLLM's block-scaled MXFP8 linear layers. Returns what happened, in one line."""
-    global _ORIG_PWAL, _ORIG_APPLY
     import importlib.util  # noqa: PLC0415
 
     if importlib.util.find_spec("vllm") is None:
         return "vllm is not importable; mxfp8 not patched"
-    if _ORIG_APPLY is not None:
+    if SWAP.active:
         return "mxfp8: already patched"
     from ..target import current_arch  # noqa: PLC0415
 
-    if current_arch() != "gfx950":
-        return f"mxfp8: not patched -- gfx950's scaled MFMA, not {current_arch()}"
+    arch = current_arch()
+    if arch != "gfx950":
+        return f"mxfp8: not patched -- the MX GEMM is gfx950's scaled MFMA, not {arch}"
     PATCH.define(mxfp8_linear)
-    cls = _cls()
-    _ORIG_PWAL, _ORIG_APPLY = cls.process_weights_after_loading, cls.apply_weights
-    cls.process_weights_after_loading = process_weights_after_loading
-    cls.apply_weights = apply_weights
+    SWAP.install(_kernel_class(), {"process_weights_after_loading": process_weights_after_loading,
+                                   "apply_weights": apply_weights})
+    cache = engine.isolate_compile_cache("mxfp8")
     t = routes()
-    return ("mxfp8 -> hk where " + (f"{t.source} measured it faster" if t is not None
-                                    else f"M >= {MIN_M}"))
+    where = f"{t.source} measured it faster" if t is not None else f"M >= {MIN_M}"
+    return f"mxfp8 -> hk where {where} (compile cache {cache})"
 
 
 def revert() -> str:
-    global _ORIG_PWAL, _ORIG_APPLY
-    if _ORIG_APPLY is None:
+    if not SWAP.active:
         return "mxfp8: not patched"
-    cls = _cls()
-    cls.process_weights_after_loading, cls.apply_weights = _ORIG_PWAL, _ORIG_APPLY
-    _ORIG_PWAL = _ORIG_APPLY = None
+    SWAP.restore()
     return "mxfp8 -> vllm"
 
 
 def status() -> str:
-    return "not patched" if _ORIG_APPLY is None else PATCH.summary()
+    return PATCH.summary() if SWAP.active else "not patched"
 
 
-__all__ = ["PATCH", "schedule", "routes", "set_routes", "mxfp8_linear", "apply_patch", "revert", "status",
-           "process_weights_after_loading", "apply_weights"]
+__all__ = ["PATCH", "schedule", "routes", "set_routes", "mxfp8_linear", "apply_patch", "revert",
+           "status", "process_weights_after_loading", "apply_weights"]

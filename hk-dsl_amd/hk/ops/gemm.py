@@ -22,9 +22,34 @@ def matmul(a, b, out=None):
     return gemm_cdna.matmul(a, b, out=out)
 
 
+#: Python-number scales as one-element fp32 device tensors, by (device, value): made once
+#: by a fill kernel (no host-to-device copy per call) and reused.
+_NUMBERS: dict = {}
+_NUMBERS_CAP = 1024
+
+
+def _number(v: float, device):
+    """A scale given as a Python number, on `device`. Outside a graph capture the tensor is
+    cached; while capturing it is made by a fill kernel the graph records (so a replay
+    refills it) and not kept, since a tensor filled only on replay would be garbage to an
+    eager call before the first replay."""
+    import torch  # noqa: PLC0415
+
+    key = (device, float(v))
+    t = _NUMBERS.get(key)
+    if t is not None:
+        return t
+    t = torch.full((1,), float(v), device=device, dtype=torch.float32)
+    if not torch.cuda.is_current_stream_capturing() and len(_NUMBERS) < _NUMBERS_CAP:
+        _NUMBERS[key] = t
+    return t
+
+
 def _vec(t, length, what, device):
     import torch  # noqa: PLC0415
 
+    if isinstance(t, (int, float)) and not isinstance(t, bool):
+        return _number(t, device), 0
     t = torch.as_tensor(t, device=device, dtype=torch.float32)
     if t.numel() == 1:
         return t.reshape(1), 0

@@ -53,6 +53,7 @@ import inspect
 import re
 import sys
 import types
+import weakref
 from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Optional, Tuple
 
@@ -164,55 +165,106 @@ class Context:
         return _trace.Sym(self._g, self._g.make("LOAD", name=name, kind=k))
 
 
+class _Signature:
+    """How an epilogue takes its arguments after the accumulator: each positional name is
+    `ctx` (the context) or an operand read by that name; each keyword-only one is a number
+    with a default that an operand of that name overrides. The contract of
+    templates/gemm.py:341-366: fn(acc), fn(acc, ctx), fn(acc, bias, residual, *, alpha=1.0)."""
+
+    __slots__ = ("positional", "numbers")
+
+    def __init__(self, fn):
+        label = getattr(fn, "__name__", repr(fn))
+        sig = inspect.signature(fn)
+        P = inspect.Parameter
+        positional, numbers = [], {}
+        for p in sig.parameters.values():
+            if p.kind in (P.VAR_POSITIONAL, P.VAR_KEYWORD):
+                positional = None
+                break
+            if p.kind is P.KEYWORD_ONLY:
+                if p.default is P.empty:
+                    raise TypeError(f"{label}: a keyword-only parameter of an epilogue is a "
+                                    f"number with a default")
+                numbers[p.name] = p.default
+            else:
+                positional.append(p.name)
+        if not positional:
+            raise TypeError(f"an epilogue is fn(acc, ...): the accumulator, then `ctx` or "
+                            f"operands by name; {label} is {sig}")
+        self.positional = tuple(positional[1:])
+        self.numbers = numbers
+
+    def invoke(self, fn, acc, ctx):
+        given = ctx._ep.kinds
+        args = [ctx if name == "ctx" else getattr(ctx, name) for name in self.positional]
+        kwargs = {name: getattr(ctx, name) if name in given else default
+                  for name, default in self.numbers.items()}
+        return fn(acc, *args, **kwargs)
+
+
+_SIGNATURES: "weakref.WeakKeyDictionary[Any, _Signature]" = weakref.WeakKeyDictionary()
+
+
+def _signature(fn) -> _Signature:
+    """`fn`'s checked signature (TypeError if it cannot be an epilogue)."""
+    try:
+        return _SIGNATURES[fn]
+    except (KeyError, TypeError):
+        pass
+    sig = _Signature(fn)
+    try:
+        _SIGNATURES[fn] = sig
+    except TypeError:
+        pass
+    return sig
+
+
 def _params(fn):
-    """(positional names after acc, keyword-only names with defaults) of an epilogue:
-    fn(acc), fn(acc, ctx), fn(acc, bias, residual, ..., *, alpha=1.0)
-    (templates/gemm.py:341-356)."""
-    ps = list(inspect.signature(fn).parameters.values())
-    pos = [p for p in ps if p.kind in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD)]
-    kw = [p for p in ps if p.kind is p.KEYWORD_ONLY]
-    if not pos or any(p.kind in (p.VAR_POSITIONAL, p.VAR_KEYWORD) for p in ps):
-        raise TypeError(f"an epilogue is fn(acc, ...): the accumulator, then `ctx` or "
-                        f"operands by name; {getattr(fn, '__name__', fn)} is "
-                        f"{inspect.signature(fn)}")
-    if any(p.default is inspect.Parameter.empty for p in kw):
-        raise TypeError(f"{getattr(fn, '__name__', fn)}: a keyword-only parameter of an "
-                        f"epilogue is a number with a default")
-    return [p.name for p in pos[1:]], {p.name: p.default for p in kw}
+    """(positional names after acc, keyword-only numbers with defaults) of an epilogue."""
+    sig = _signature(fn)
+    return list(sig.positional), dict(sig.numbers)
 
 
 def _call(fn, acc, ctx):
-    """Call `fn` on acc, binding `ctx`, operands by name, keyword-only numbers
-    (templates/gemm.py:359-366)."""
-    pos, kw = _params(fn)
-    args = [ctx if n == "ctx" else getattr(ctx, n) for n in pos]
-    kws = {n: (getattr(ctx, n) if n in ctx._ep.kinds else d) for n, d in kw.items()}
-    return fn(acc, *args, **kws)
+    """`fn` applied to the tile `acc`, its parameters bound from `ctx`; None means `acc`."""
+    got = _signature(fn).invoke(fn, acc, ctx)
+    return acc if got is None else got
+
+
+def _value_key(v) -> str:
+    if isinstance(v, (bool, int, float, str, type(None))):
+        return repr(v)
+    if isinstance(v, tuple):
+        return "(" + ",".join(_value_key(x) for x in v) + ")"
+    if callable(v):
+        return _fn_key(v)
+    return type(v).__qualname__
 
 
 def _fn_key(fn) -> str:
-    """A function's identity across processes: its source (or byte code) and what its
-    closure holds (templates/gemm.py:369-391)."""
-    if fn in _CHAINS:
-        return "chain(" + ",".join(_fn_key(f) for f in _CHAINS[fn]) + ")"
-    if fn in _INITS:
-        return f"init_from({_INITS[fn][0]}, {_fn_key(_INITS[fn][1])})"
+    """An epilogue's identity that holds across processes, for the binding's tag: a
+    composed epilogue by its parts; a function by where it is defined, its byte code and
+    constants, and the values its closure holds; anything else by repr."""
+    if isinstance(fn, _Composed):
+        return fn.key()
     code = getattr(fn, "__code__", None)
     if code is None:
         return repr(fn)
-    try:
-        text = inspect.getsource(fn)
-    except (OSError, TypeError):
-        text = code.co_code.hex() + repr(code.co_names)
+    digest = hashlib.sha1(code.co_code)
+    digest.update(repr(code.co_names).encode())
+    digest.update(",".join(_value_key(c) for c in code.co_consts
+                           if not inspect.iscode(c)).encode())
+    for sub in code.co_consts:        # nested functions and lambdas
+        if inspect.iscode(sub):
+            digest.update(sub.co_code)
     cells = []
-    for c in getattr(fn, "__closure__", None) or ():
+    for cell in fn.__closure__ or ():
         try:
-            v = c.cell_contents
-        except ValueError:
-            v = None
-        cells.append(_fn_key(v) if callable(v) else repr(v) if isinstance(
-            v, (int, float, str, bool, type(None), tuple)) else type(v).__name__)
-    return f"{fn.__module__}.{fn.__qualname__}:{text}:{cells}"
+            cells.append(_value_key(cell.cell_contents))
+        except ValueError:            # an empty cell
+            cells.append("<empty>")
+    return f"{fn.__module__}.{fn.__qualname__}#{digest.hexdigest()[:16]}[{';'.join(cells)}]"
 
 
 class Epilogue:
@@ -229,10 +281,9 @@ class Epilogue:
         self.out_dtype = out_dtype
         self.uses_coords = False
         self.paired = fn is silu_and_mul
-        inner = _INITS[fn][1] if fn in _INITS else fn
         if not self.paired:
-            _params(inner)
-        self.init = _INITS[fn][0] if fn in _INITS else None
+            _signature(fn)
+        self.init = fn.init if isinstance(fn, _Composed) else None
         if self.init is not None and kinds.get(self.init) != TILE:
             raise ValueError(
                 f"the epilogue starts the accumulator as ctx.{self.init} (init_from), so "
@@ -254,9 +305,8 @@ class Epilogue:
         acc = _trace.Sym(g, g.make("ACC", kind=_trace.TILEV))
         if self.init is not None:
             acc = acc + getattr(ctx, self.init)
-        fn = _INITS[self.fn][1] if self.fn in _INITS else self.fn
-        got = _call(fn, acc, ctx)
-        got = acc if got is None else got
+        body = self.fn.stages_call if isinstance(self.fn, _Composed) else self.fn
+        got = _call(body, acc, ctx)
         if not isinstance(got, _trace.Sym) or got.node.kind != _trace.TILEV:
             what = getattr(got, "node", None)
             raise TypeError(
@@ -706,53 +756,85 @@ def silu_and_mul(acc, ctx=None):
                     "gemm(x, w_gate_up, epilogue=gemm.silu_and_mul)")
 
 
-def chain(*fns: Callable) -> Callable:
-    """One epilogue that applies `fns` in order, each to what the last returned, all
-    reading the same ctx (templates/gemm.py:891-915)."""
-    if any(f in _INITS for f in fns[1:]):
-        raise ValueError("chain: an init_from epilogue starts the accumulator, so it can only "
-                         "come first")
-    if fns and fns[0] in _INITS:
-        name, first = _INITS[fns[0]]
-        return init_from(name)(chain(first, *fns[1:]))
-    for f in fns:
-        _params(f)
+class _Composed:
+    """An epilogue built from others: optionally an (M, N) operand the accumulator starts
+    from (`init`), then `stages` applied in order, each to what the previous returned, all
+    reading the same ctx. What `chain` and `init_from` return."""
 
-    def chained(acc, ctx):
-        for f in fns:
-            got = _call(f, acc, ctx)
-            acc = acc if got is None else got
+    def __init__(self, stages: Tuple[Callable, ...], init: Optional[str], name: str,
+                 qualname: str, doc: Optional[str] = None):
+        for f in stages:
+            _signature(f)
+        self.stages = tuple(stages)
+        self.init = init
+        self.__name__ = name
+        self.__qualname__ = qualname
+        self.__doc__ = doc
+
+    def stages_call(self, acc, ctx):
+        """The stages alone, the accumulator already started from `init`."""
+        for f in self.stages:
+            acc = _call(f, acc, ctx)
         return acc
 
-    chained.__name__ = "_".join(getattr(f, "__name__", "fn") for f in fns)
-    chained.__qualname__ = "chain(" + ", ".join(getattr(f, "__qualname__", "?") for f in fns) + ")"
-    _CHAINS[chained] = fns
-    return chained
+    def __call__(self, acc, ctx):
+        return self.stages_call(acc, ctx)
+
+    def key(self) -> str:
+        inner = ",".join(_fn_key(f) for f in self.stages)
+        return f"init_from({self.init})[{inner}]" if self.init else f"chain[{inner}]"
+
+    def __repr__(self) -> str:
+        return f"<epilogue {self.__qualname__}>"
 
 
-_CHAINS: Dict[Callable, Tuple] = {}
-_INITS: Dict[Callable, Tuple[str, Callable]] = {}
+def _label(f, attr="__name__") -> str:
+    return getattr(f, attr, None) or type(f).__name__
+
+
+def chain(*fns: Callable) -> Callable:
+    """One epilogue that applies `fns` in order, each to what the previous returned, all
+    reading the same ctx (templates/gemm.py:891-915). An `init_from` epilogue may only
+    come first: it decides where the accumulator starts."""
+    for f in fns[1:]:
+        if isinstance(f, _Composed) and f.init:
+            raise ValueError("chain: an init_from epilogue starts the accumulator, so it can "
+                             "only come first")
+    init = None
+    stages: List[Callable] = []
+    for i, f in enumerate(fns):
+        if i == 0 and isinstance(f, _Composed) and f.init:
+            init = f.init
+            stages.extend(f.stages)
+        else:
+            stages.append(f)
+    name = "_".join(_label(f) for f in fns)
+    qual = "chain(" + ", ".join(_label(f, "__qualname__") for f in fns) + ")"
+    if init:
+        qual = f"init_from({init!r})({qual})"
+    return _Composed(tuple(stages), init, name, qual)
 
 
 def init_from(name: str) -> Callable:
     """Decorator: the accumulator starts as the (M, N) operand `name` instead of zero, so
-    C = fn(name + A @ B^T, ctx) -- BLAS's beta * C with beta 1 (templates/gemm.py:924-945)."""
+    C = fn(name + A @ B^T, ctx) -- BLAS's beta * C with beta 1 (templates/gemm.py:924-945).
+    The kernels add it where they store, in fp32, before the epilogue."""
     if not isinstance(name, str) or not name.isidentifier():
         raise TypeError(f"init_from takes an operand's name, not {name!r}")
 
-    def deco(fn):
-        _params(fn)
+    def start_from(fn):
+        if isinstance(fn, _Composed):
+            if fn.init:
+                raise ValueError(f"init_from({name!r}): {fn.__qualname__} already starts "
+                                 f"from {fn.init!r}")
+            stages = fn.stages
+        else:
+            stages = (fn,)
+        return _Composed(stages, name, _label(fn),
+                         f"init_from({name!r})({_label(fn, '__qualname__')})",
+                         getattr(fn, "__doc__", None))
 
-        def wrapped(acc, ctx):
-            return _call(fn, acc, ctx)
-
-        wrapped.__name__ = getattr(fn, "__name__", "fn")
-        wrapped.__qualname__ = f"init_from({name!r})({getattr(fn, '__qualname__', '?')})"
-        wrapped.__doc__ = getattr(fn, "__doc__", None)
-        _INITS[wrapped] = (name, fn)
-        return wrapped
-
-    return deco
+    return start_from
 
 
 residual = init_from("residual")(_residual)
@@ -762,54 +844,49 @@ READY = {f.__name__: f for f in (bias, gelu, silu, relu, bias_gelu, bias_silu, b
                                  residual, bias_residual, scale, gelu_tanh, silu_and_mul)}
 
 
-class _Gemm:
-    """hk.templates.gemm(a, b, epilogue=fn, out=None, out_dtype=None, **operands) -> C;
-    with no a and b, the same bound to its keywords, to call later."""
+class _Bound:
+    """gemm(epilogue=..., **operands) with no A and B: the same call waiting for them.
+    Calling it with (a, b) and optionally out= and more operands launches."""
 
-    plan = staticmethod(plan)
-    kernels = staticmethod(kernels)
-    kernel_for = staticmethod(kernel_for)
-    chain = staticmethod(chain)
-    init_from = staticmethod(init_from)
-    Context = Context
-    Step = Step
+    def __init__(self, epilogue, out, out_dtype, schedule, operands):
+        self._epilogue, self._out, self._out_dtype = epilogue, out, out_dtype
+        self._schedule, self._operands = schedule, operands
+        self.__name__ = f"gemm[{getattr(epilogue, '__name__', 'plain')}]"
 
-    def __init__(self):
-        for name, f in READY.items():
-            setattr(self, name, f)
+    def __call__(self, a, b, *, out=None, **more):
+        ops = dict(self._operands)
+        ops.update(more)
+        return _gemm(a, b, epilogue=self._epilogue,
+                     out=self._out if out is None else out,
+                     out_dtype=self._out_dtype, schedule=self._schedule, **ops)
+
+    def __repr__(self) -> str:
+        return f"<{self.__name__}>"
+
+
+class _GemmModule(types.ModuleType):
+    """This module is itself the template: `hk.templates.gemm(a, b, ...)` -- and, after
+    `import hk.templates.gemm`, the module that name now binds -- launches, and its
+    attributes (the ready-made epilogues, `plan`, `kernels`, `kernel_for`, `chain`,
+    `init_from`, `Context`, `Step`) are the module's own (templates/gemm.py:956-1004)."""
 
     def __call__(self, a=None, b=None, *, epilogue=None, out=None, out_dtype=None,
                  schedule=None, **operands):
         if a is None and b is None:
-            def bound(a, b, *, out=out, **more):
-                return _gemm(a, b, epilogue=epilogue, out=out, out_dtype=out_dtype,
-                             schedule=schedule, **{**operands, **more})
-
-            bound.__name__ = f"gemm[{getattr(epilogue, '__name__', 'plain')}]"
-            return bound
+            return _Bound(epilogue, out, out_dtype, schedule, operands)
         if a is None or b is None:
             raise TypeError("hk.templates.gemm(a, b, ...) takes both A and B, or neither (to "
                             "bind the epilogue for later)")
-        return _gemm(a, b, epilogue=epilogue, out=out, out_dtype=out_dtype, schedule=schedule,
-                     **operands)
+        return _gemm(a, b, epilogue=epilogue, out=out, out_dtype=out_dtype,
+                     schedule=schedule, **operands)
 
     def __repr__(self) -> str:
         return "<hk.templates.gemm>"
 
 
-gemm = _Gemm()
-gemm.__doc__ = __doc__
-
-
-class _CallableModule(types.ModuleType):
-    """`import hk.templates.gemm` binds the package's attribute to this module, so the
-    module calls through too, with the same attributes (templates/gemm.py:996-1004)."""
-
-    def __call__(self, *args, **kwargs):
-        return gemm(*args, **kwargs)
-
-
-sys.modules[__name__].__class__ = _CallableModule
+sys.modules[__name__].__class__ = _GemmModule
+#: The template (this module): `from hk.templates.gemm import gemm` works too.
+gemm = sys.modules[__name__]
 
 __all__ = ["gemm", "plan", "kernels", "kernel_for", "bind", "init_from", "Step", "Context",
            "Epilogue", "chain", "READY", *READY]

@@ -88,20 +88,24 @@ def test_route_for(routed):
 
 
 def test_no_table_routes_nothing():
-    V.set_routes(None)
-    V._TABLE.append(None)
+    V.ROUTER.replace(None, loaded=True)     # an arch with no table
     try:
+        assert V.routes() is None
         assert V.route_for(64, 4096, 4096) == "fallback"
     finally:
-        V._TABLE.clear()
+        V.set_routes(None)
 
 
 def test_cpu_tensors_and_fallback_compute_linear(routed):
     x = torch.randn(3, 5, 64)
     w = torch.randn(1000, 64)
     b = torch.randn(1000)
-    y = V._gemm(None, x, w, b)  # a CPU tensor never leaves torch
-    torch.testing.assert_close(y, torch.nn.functional.linear(x, w, b))
+    w_routed = torch.randn(4096, 4096, dtype=torch.bfloat16)
+    xr = torch.ones(3, 4096, dtype=torch.bfloat16)
+    layer = types.SimpleNamespace()
+    y = V._layer_gemm(None, layer, xr, w_routed)                # routed, but on the CPU:
+    torch.testing.assert_close(y, torch.nn.functional.linear(xr, w_routed))
+    assert layer._hk_route == (V.ROUTER.generation, "")            # torch's own GEMM
     V.PATCH.reset()
     y2 = V.linear(x.bfloat16(), w.bfloat16(), None)  # the table sends (1000, 64) to the fallback
     assert V.PATCH.stats["fallback"] == 1
@@ -134,15 +138,18 @@ def test_dispatch_rebinding_with_a_stand_in_vllm(routed, monkeypatch):
     mods["vllm.model_executor.layers"].utils = utils
     for k, v in mods.items():
         monkeypatch.setitem(sys.modules, k, v)
+    monkeypatch.setenv("VLLM_CACHE_ROOT", "/tmp/vllm-cache")
     msg = V.apply()
     assert "2 rebound" in msg, msg
+    assert "compile cache /tmp/vllm-cache/hk-linear" in msg
+    assert __import__("os").environ["VLLM_CACHE_ROOT"] == "/tmp/vllm-cache/hk-linear"
     assert utils.dispatch_unquantized_gemm is V.dispatch_unquantized_gemm
     assert other.dispatch_unquantized_gemm is V.dispatch_unquantized_gemm
     g = utils.dispatch_unquantized_gemm()
     layer = types.SimpleNamespace()
-    w = torch.randn(1000, 64)
-    g(layer, torch.randn(2, 64), w)  # a shape the table never routes: vLLM's own GEMM
-    assert calls == ["orig"] and layer._hk_gemm[1] is False
+    w = torch.randn(1000, 64, dtype=torch.bfloat16)
+    g(layer, torch.randn(2, 64, dtype=torch.bfloat16), w)  # a shape the table never routes
+    assert calls == ["orig"] and layer._hk_route[1] == "no route at any M"
     assert "2 rebound" in V.revert()
     assert utils.dispatch_unquantized_gemm is orig_dispatch
 
@@ -166,7 +173,7 @@ def test_vllm_mxfp8_route_and_patch_without_vllm():
 
     # without a table: M >= MIN_M
     V.set_routes(None)
-    V._TABLE.append(None)
+    V._TABLE.append(None)      # no table for this arch
     try:
         assert V.schedule(V.MIN_M, 5120, 4096)
         assert not V.schedule(V.MIN_M - 1, 5120, 4096)
@@ -190,3 +197,121 @@ def test_vllm_mxfp8_route_and_patch_without_vllm():
     if importlib.util.find_spec("vllm") is None:
         assert "not importable" in V.apply_patch()
     assert V.revert() == "mxfp8: not patched"
+
+
+def test_compile_cache_isolation_merges_routes(monkeypatch, tmp_path):
+    """Each patched engine gets its own vLLM cache root under the current one, named for
+    every route applied in any order, and a worker that inherits it adds nothing."""
+    monkeypatch.setenv("VLLM_CACHE_ROOT", str(tmp_path / "vc"))
+    assert engine.isolate_compile_cache("mxfp8") == str(tmp_path / "vc" / "hk-mxfp8")
+    assert engine.isolate_compile_cache("linear") == str(tmp_path / "vc" / "hk-linear+mxfp8")
+    assert engine.isolate_compile_cache("mxfp8") == str(tmp_path / "vc" / "hk-linear+mxfp8")
+    monkeypatch.delenv("VLLM_CACHE_ROOT")
+    monkeypatch.setenv("XDG_CACHE_HOME", str(tmp_path / "xdg"))
+    assert engine.isolate_compile_cache("linear") == str(tmp_path / "xdg" / "vllm" / "hk-linear")
+
+
+# ------------------------------------------------- the compiled forward's contract
+#
+# vLLM compiles its forward whole (fullgraph) and refuses to start when the code Dynamo
+# produces names `update` (compilation/wrapper.py's bytecode hook): a write the graph must
+# replay afterwards is lost on a CUDA-graph replay. The forward below has the shape of
+# vLLM's UnquantizedLinearMethod.apply -- call dispatch_unquantized_gemm(), then the GEMM
+# it returns -- and runs on the CPU with a stand-in for vLLM's own dispatch (x2, so which
+# GEMM ran is visible in the output). The reference's check of the same contract is
+# tests/hk/ir/test_vllm_gemm_compiled.py:85-125.
+
+NC, KC = 256, 128
+
+
+def _engine_dispatch(*args, **kwargs):
+    return lambda layer, x, weight, bias=None: torch.nn.functional.linear(x, weight, bias) * 2
+
+
+class _Layer(torch.nn.Module):
+    def __init__(self, dtype):
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.randn(NC, KC).to(dtype), requires_grad=False)
+
+    def forward(self, x):
+        return V.dispatch_unquantized_gemm()(self, x.to(self.weight.dtype), self.weight, None)
+
+
+class _Net(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.layers = torch.nn.ModuleList([_Layer(torch.bfloat16), _Layer(torch.float16),
+                                           _Layer(torch.bfloat16)])
+
+    def forward(self, x):
+        return sum(layer(x).float() for layer in self.layers)
+
+
+@pytest.fixture
+def stand_in_engine(monkeypatch):
+    monkeypatch.setattr(V, "_VLLM_DISPATCH", _engine_dispatch)
+    monkeypatch.setattr(V, "UNROUTED", V.Counter())
+    V.set_routes(engine.RouteTable({(NC, KC): {"runs": [[1, 64, "hk_decode"]], "above": "hk"}}))
+    yield
+    V.set_routes(None)
+
+
+def _compile_and_watch(model, x):
+    """Compile `model` whole as vLLM does; return (output, names of the frames whose
+    transformed code names `update`)."""
+    flagged = []
+
+    def hook(old, new):
+        if "update" in new.co_names:
+            flagged.append(old.co_name)
+
+    torch._dynamo.reset()
+    handle = torch._dynamo.convert_frame.register_bytecode_hook(hook)
+    try:
+        out = torch.compile(model, fullgraph=True, backend="eager")(x)
+    finally:
+        handle.remove()
+        torch._dynamo.reset()
+    return out, flagged
+
+
+def _state(model):
+    return ([getattr(layer, "_hk_route", None) for layer in model.layers], dict(V.UNROUTED),
+            dict(V.ROUTER.plans))
+
+
+@pytest.mark.parametrize("decided", ["at load", "never", "for a replaced table"])
+def test_the_compiled_forward_writes_nothing(stand_in_engine, decided):
+    model = _Net()
+    if decided != "never":
+        for layer in model.layers:
+            V._layer_routed(layer, layer.weight, None)
+    if decided == "for a replaced table":
+        V.set_routes(V.routes())            # a new generation: every kept decision is stale
+    before = _state(model)
+    x = torch.randn(4, KC)
+    out, flagged = _compile_and_watch(model, x)
+    assert flagged == [], f"the traced forward writes state vLLM's guard refuses: {flagged}"
+    assert _state(model) == before           # no decision, count or plan kept by the trace
+    torch.testing.assert_close(out, model(x))
+
+
+def test_the_compiled_forward_routes_as_eager_does(stand_in_engine):
+    """Traced, the bf16 layers go through the op's CPU path (F.linear) and the fp16 one
+    to the engine's GEMM (x2 in the stand-in)."""
+    model = _Net()
+    x = torch.randn(4, KC)
+    out, _ = _compile_and_watch(model, x)
+    want = sum(torch.nn.functional.linear(x.to(l.weight.dtype), l.weight).float()
+               * (2 if l.weight.dtype == torch.float16 else 1) for l in model.layers)
+    torch.testing.assert_close(out, want, rtol=2e-2, atol=2e-1)
+
+
+def test_eager_forward_decides_each_layer_once(stand_in_engine):
+    model = _Net()
+    model(torch.randn(4, KC))
+    model(torch.randn(4, KC))
+    gen = V.ROUTER.generation
+    assert [layer._hk_route for layer in model.layers] == [
+        (gen, ""), (gen, "weight float16"), (gen, "")]
+    assert V.UNROUTED == {"weight float16": 1}

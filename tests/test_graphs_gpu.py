@@ -71,3 +71,41 @@ def test_single_pass_graph_replays(sched):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}"
+
+
+@pytest.mark.parametrize("scalar_first", [False, True])
+def test_scaled_mm_with_number_scales_replays(scalar_first):
+    """scaled_mm with Python-number scales under capture: the numbers become device
+    tensors by a fill kernel (no host-to-device copy, which a capture refuses). Captured
+    both with the scale tensors already made eagerly (scalar_first) and with the first
+    sight of the numbers inside the capture; every replay equals the eager result and
+    the oracle."""
+    from hk.ops import gemm as G
+    from oracle import gemm_oracle as O
+
+    m, n, k = 512, 1024, 1024
+    gen = torch.Generator().manual_seed(42)
+    a8 = (torch.randn(m, k, generator=gen) * 4).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(n, k, generator=gen) * 4).to(torch.float8_e4m3fn)
+    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    sa, sb = 0.375 + 0.001 * scalar_first, 0.0625
+    ad, bd, biasd = a8.to(DEV), b8.to(DEV), bias.to(DEV)
+    G._NUMBERS.clear()
+    if scalar_first:
+        ref = G.scaled_mm(ad, bd, sa, sb, bias=biasd).clone()
+    out = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    G.scaled_mm(ad, bd, 1.0, 1.0, bias=biasd, out=out)     # warm up with other numbers
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        G.scaled_mm(ad, bd, sa, sb, bias=biasd, out=out)
+    if not scalar_first:
+        assert (G._NUMBERS.keys() & {(ad.device, sa), (ad.device, sb)}) == set()
+        ref = G.scaled_mm(ad, bd, sa, sb, bias=biasd).clone()
+    O.assert_close(ref, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+    for rep in range(3):
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"
