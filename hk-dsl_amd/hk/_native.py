@@ -177,22 +177,27 @@ def workspace(device, nbytes: int):
     reference's module-owned scratch (python/hk/ops/gemm_cdna_dp.py:330-338). Calls on
     one stream run in order, so they can share it.
 
-    Under CUDA-graph capture a graph bakes the buffer's address in, so a buffer a capture
-    has used is never freed: it is pinned for the life of the process (a bigger one for a
-    later call replaces it in the cache, not in memory). Otherwise a buffer replaced by a
-    bigger one is freed, and torch.cuda.graph's empty_cache() before the next capture can
-    unmap it under a graph that still replays it."""
+    Under CUDA-graph capture a graph bakes the buffer's address in, so each captured call
+    gets a buffer of its own that is never freed (kept for the life of the process): a
+    shared one could be freed when a bigger one replaced it in the cache -- and
+    torch.cuda.graph's empty_cache() before the next capture would unmap it under a graph
+    that still replays it -- and two graphs replayed at once on different streams would
+    race on it."""
     import torch  # noqa: PLC0415
 
     if nbytes == 0:
         return None
+    if capturing(device):
+        # a buffer of this capture's own, kept for the life of the process: two graphs
+        # replayed at once on different streams must not share one
+        buf = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+        _PINNED.append(buf)
+        return buf
     key = (device, stream_of(device))
     buf = _WS.get(key)
     if buf is None or buf.numel() * 4 < nbytes:
         buf = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
         _WS[key] = buf
-    if capturing(device) and not any(b is buf for b in _PINNED):
-        _PINNED.append(buf)
     return buf
 
 
@@ -228,5 +233,5 @@ def run(args: HkxGemmArgs, device) -> None:
     check(L.hkx_gemm(ctypes.byref(args), c_void_p(stream_of(device))))
 
 
-__all__ = ["lib", "check", "HkxError", "HkxGemmArgs", "HkxEpilogue", "HkxOperand", "HkxInstr",
+__all__ = ["lib", "check",  "HkxError", "HkxGemmArgs", "HkxEpilogue", "HkxOperand", "HkxInstr",
            "gemm_args", "run", "workspace", "dtype_code", "SYMBOLS", "OP", "OPS"]
