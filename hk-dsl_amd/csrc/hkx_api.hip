@@ -13,6 +13,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "hkx.h"
@@ -376,6 +377,35 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
   return hkx::launch_tile<256, 128, 4>(t, fp8, mode, grid, s);
 }
 
+// The fp32 workspace of hkx_gemm_noalloc: a file-scope device array, so a call needs no
+// allocation. Each GPU the library runs on holds its own copy (HKX_NOALLOC_SCRATCH_BYTES)
+// until the process ends. In host code `scratch` names a host-side stand-in, not device
+// memory: the kernels get the per-device address hipGetSymbolAddress returns.
+__device__ __align__(256) unsigned char scratch[HKX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch` (looked up once per device, that device current).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HKX_ERR_LAUNCH, "gemm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(HKX_ERR_ARG, "gemm_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(HKX_ERR_LAUNCH, "gemm_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                  dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HKX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -595,6 +625,26 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
     if (rc) return rc;
   }
   return HKX_OK;
+}
+
+int hkx_gemm_noalloc(const HkxGemmArgs* args, void* stream) {
+  g_err.clear();
+  if (!args) return fail(HKX_ERR_ARG, "gemm_noalloc: args is NULL");
+  HkxGemmArgs a = *args;
+  a.ws = nullptr;
+  a.ws_bytes = 0;
+  const size_t need = hkx_gemm_workspace(&a);
+  if (need > (size_t)HKX_NOALLOC_SCRATCH_BYTES)
+    return fail(HKX_ERR_WORKSPACE,
+                "gemm_noalloc: this plan needs %zu bytes of workspace; the no-allocation entry "
+                "point has %zu (call hkx_gemm with a workspace, or split the call)",
+                need, (size_t)HKX_NOALLOC_SCRATCH_BYTES);
+  if (need) {
+    int rc = scratch_for_current_device(&a.ws);
+    if (rc) return rc;
+    a.ws_bytes = HKX_NOALLOC_SCRATCH_BYTES;
+  }
+  return hkx_gemm(&a, stream);
 }
 
 // The MX GEMM's K split: where its 256 x 256 tiles fill less than half the CUs, up to 8

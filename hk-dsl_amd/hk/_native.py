@@ -74,7 +74,7 @@ class HkxGemmArgs(Structure):
 #: Every function include/hkx.h declares.
 SYMBOLS = ("hkx_abi_version", "hkx_abi_sizes", "hkx_last_error", "hkx_gemm_workspace",
            "hkx_gemm_check", "hkx_gemm", "hkx_scaled_mm", "hkx_mx_gemm", "hkx_mx_gemm_workspace",
-           "hkx_mx_quant")
+           "hkx_mx_quant", "hkx_gemm_noalloc")
 
 _LIB = None
 _LOCK = threading.Lock()
@@ -113,6 +113,7 @@ def lib() -> ctypes.CDLL:
         L.hkx_gemm_workspace.restype = c_size_t
         L.hkx_gemm_check.argtypes = [POINTER(HkxGemmArgs)]
         L.hkx_gemm.argtypes = [POINTER(HkxGemmArgs), c_void_p]
+        L.hkx_gemm_noalloc.argtypes = [POINTER(HkxGemmArgs), c_void_p]
         L.hkx_mx_gemm.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32,
                                   c_int32, c_void_p, c_size_t, c_void_p]
@@ -233,5 +234,16 @@ def run(args: HkxGemmArgs, device) -> None:
     check(L.hkx_gemm(ctypes.byref(args), c_void_p(stream_of(device))))
 
 
-__all__ = ["lib", "check",  "HkxError", "HkxGemmArgs", "HkxEpilogue", "HkxOperand", "HkxInstr",
+#: The no-allocation entry point's scratch per GPU (HKX_NOALLOC_SCRATCH_BYTES in hkx.h).
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def run_noalloc(args: HkxGemmArgs, device) -> None:
+    """Launch `args` through hkx_gemm_noalloc on `device`'s current stream: the workspace
+    is the library's static per-GPU scratch, so nothing is allocated (calls overlapping on
+    one GPU race on that scratch)."""
+    check(lib().hkx_gemm_noalloc(ctypes.byref(args), c_void_p(stream_of(device))))
+
+
+__all__ = ["lib", "check", "run_noalloc", "NOALLOC_SCRATCH_BYTES", "HkxError", "HkxGemmArgs", "HkxEpilogue", "HkxOperand", "HkxInstr",
            "gemm_args", "run", "workspace", "dtype_code", "SYMBOLS", "OP", "OPS"]

@@ -233,6 +233,19 @@ int hkx_gemm_check(const HkxGemmArgs* args);
  * Returns HKX_OK or an error code; hkx_last_error() says why. */
 int hkx_gemm(const HkxGemmArgs* args, void* stream);
 
+/* hkx_gemm with no workspace argument and no allocation: the plan's fp32 workspace (split-K
+ * shares, a register program's sum) is a static device array of the library,
+ * HKX_NOALLOC_SCRATCH_BYTES on each GPU it runs on, held until the process ends. args->ws
+ * and args->ws_bytes are ignored. A plan that needs more than that fails with
+ * HKX_ERR_WORKSPACE (nothing launched). Calls no hipMalloc / hipFree; every kernel writes
+ * each scratch byte it reads in the same call, so nothing needs clearing between calls.
+ * Every call on one GPU shares that GPU's array: two calls that overlap in time on one GPU
+ * (other streams, or graphs replayed concurrently) race on it -- serialise them.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP-graph capture, serving loops and harnesses that forbid hipMalloc). */
+#define HKX_NOALLOC_SCRATCH_BYTES (64u << 20)
+int hkx_gemm_noalloc(const HkxGemmArgs* args, void* stream);
+
 /* bf16 C = (A . B^T) * scale_a * scale_b (+ bias), A (M, K) and B (N, K) fp8-e4m3,
  * scale_a fp32 with sa_ld 0 (one value for all rows: per-tensor) or its row
  * stride (per-token, (M, 1)); scale_b fp32, sb_per_channel 0 (one value) or 1
