@@ -175,6 +175,7 @@ def main():
     torch.testing.assert_close(out.float(), ref, rtol=1e-2, atol=1e-2)
     del ref
     flops = 2.0 * m * n * k
+    peaks = measured_peaks()
     mean_s, med_s, wall = _events_time(step, args.steps, args.warmup)
     value = flops * args.steps / wall / 1e12
     achieved = flops / mean_s / 1e12
@@ -198,6 +199,8 @@ def main():
                    "route": plan[0].route, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
+                     "peak_measured": peaks["mfma_bf16_tflops"],
+                     "frac_measured": round(achieved / peaks["mfma_bf16_tflops"], 4),
                      "kernel": kname,
                      "avg_launch_us": round(mean_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
                      "algorithmic_flops_per_launch": flops},
@@ -210,8 +213,9 @@ def main():
             rec = json.load(f)
         if rec.get("kernel") == kname:
             res["roofline"]["traffic"] = rec.get("hbm_bytes_per_launch")
+    res["measured_peaks"] = peaks
     if not args.quick:
-        res["also"] = other_configs(args.steps, args.warmup)
+        res["also"] = other_configs(args.steps, args.warmup, peaks)
         del x, wt, b, out
         torch.cuda.empty_cache()
         res["cpu_baseline"] = cpu_baseline(*_inputs(m, k, n, 0, "cpu"))
@@ -227,7 +231,20 @@ def main():
     print(json.dumps(res), flush=True)
 
 
-def other_configs(steps, warmup):
+def measured_peaks():
+    """This GPU's own ceilings, measured in this run with the build's probe (hk.peaks):
+    the dense MFMA rate of a register-only loop (bf16, fp8) and the HBM read rate of one
+    pass over 2 GiB (past the 256 MB Infinity Cache). Each is the best of 5 launches."""
+    from hk import peaks
+
+    return {"mfma_bf16_tflops": round(peaks.mfma_tflops(False), 1),
+            "mfma_fp8_tflops": round(peaks.mfma_tflops(True), 1),
+            "hbm_read_gbs": round(peaks.hbm_read_gbs(), 1),
+            "how": "hk.peaks: register-only 32x32 MFMA loop on every CU; one pass of 16-byte "
+                   "non-temporal reads over 2 GiB"}
+
+
+def other_configs(steps, warmup, peaks):
     """Configs 3-5, timed as config 2 is (HIP events per launch, mean)."""
     import torch
 
@@ -244,6 +261,7 @@ def other_configs(steps, warmup):
         fl = 2.0 * m * 24576 * 4096
         out[f"cfg3_gate_up_silu_mul_M{m}"] = {"TFLOP/s": round(fl / t / 1e12, 1),
                                               "frac_bf16_peak": round(fl / t / 1e12 / PEAK_BF16, 4),
+                                              "frac_measured": round(fl / t / 1e12 / peaks["mfma_bf16_tflops"], 4),
                                               "us": round(t * 1e6, 1)}
         del x, wt, y
     # config 4: decode, 4 weight copies (403 MB) rotated past the 256 MB MALL; kernel time
@@ -263,6 +281,7 @@ def other_configs(steps, warmup):
             byts = 12288 * 4096 * 2 + m * 4096 * 2 + m * 12288 * 2 + (12288 * 2 if epi == "bias" else 0)
             out[f"cfg4_decode_M{m}_{epi}"] = {"GB/s": round(byts / t / 1e9, 1),
                                               "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM, 4),
+                                              "frac_measured": round(byts / t / 1e9 / peaks["hbm_read_gbs"], 4),
                                               "us": round(t * 1e6, 2)}
     del ws
     # config 5: fp8 e4m3 scaled GEMM + dequant + bias
@@ -277,6 +296,7 @@ def other_configs(steps, warmup):
     fl = 2.0 * 8192 * 4096 * 4096
     out["cfg5_fp8_scaled_dequant_bias"] = {"TFLOP/s": round(fl / t / 1e12, 1),
                                            "frac_fp8_peak": round(fl / t / 1e12 / PEAK_FP8, 4),
+                                           "frac_measured": round(fl / t / 1e12 / peaks["mfma_fp8_tflops"], 4),
                                            "us": round(t * 1e6, 1)}
     return out
 

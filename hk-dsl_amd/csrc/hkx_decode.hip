@@ -45,19 +45,38 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
 
 bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
   const int groups = a.g_total;  // 128-element K groups
-  return splits == 1 && !pair && a.M <= 16 && groups % 8 == 0 && groups <= 256;
+  const bool tile_operand = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
+  return splits == 1 && !pair && !tile_operand && a.M <= 16 && groups % 8 == 0 && groups <= 256;
+}
+
+// Whether the stream kernel's fast epilogue form takes the call's epilogue: no tile or
+// vector scales (broadcast ones are fine), a bias -- if any -- bf16 of unit stride, 4-byte
+// aligned, N even.
+static bool stream_fast(const DecodeArgs& a) {
+  const Fused& e = a.ep;
+  if (e.form != HKX_EP_FUSED) return true;
+  if ((e.cs.p && e.cs.ld) || (e.rs.p && e.rs.ld) || e.ta.p) return false;
+  if (e.ra.p && e.ra.ld)
+    return e.ra.dt == HKX_BF16 && e.ra.ld == 1 && ((uintptr_t)e.ra.p & 3) == 0 && a.N % 2 == 0;
+  return true;
+}
+
+template <int EPF>
+static hipError_t launch_stream_ep(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(512);
+  switch (a.g_total / 8) {
+    case 1: hipLaunchKernelGGL((stream_kernel<1, EPF>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((stream_kernel<2, EPF>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((stream_kernel<3, EPF>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((stream_kernel<4, EPF>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((stream_kernel<0, EPF>), grid, block, 0, s, a); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  const dim3 block(512);
-  switch (a.g_total / 8) {
-    case 1: hipLaunchKernelGGL((stream_kernel<1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((stream_kernel<2>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((stream_kernel<3>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((stream_kernel<4>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((stream_kernel<0>), grid, block, 0, s, a); break;
-  }
-  return hipGetLastError();
+  return stream_fast(a) ? launch_stream_ep<kStreamEpFast>(a, grid, s)
+                        : launch_stream_ep<kStreamEpGeneric>(a, grid, s);
 }
 
 }  // namespace hkx

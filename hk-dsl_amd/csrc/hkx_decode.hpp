@@ -163,8 +163,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 }
 
 
-// The streaming decode GEMM: one workgroup a CU walks the 16-row blocks of W (every
-// gridDim.x-th), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
+// The streaming decode GEMM: one workgroup a CU walks its share of the 16-row blocks of W
+// (a consecutive run of them), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
 // 1024: CPB chunks of 1024 a block (CPB = 1..4), or, with CPB = 0, K / 1024 of them read
 // at run time (K past 4096).
 //
@@ -180,10 +180,24 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 //   the first block's fill of the chunk before it (all of X up front cost 1 us of
 //   20 at M = 16, K = 4096); past K = 4096 it is streamed with the chunks instead (two
 //   chunks ahead, three register slots).
+//   Each step issues its X loads before its fill, so the waits, which count loads in issue
+//   order, wait for exactly the chunk and the X they need (the compiler's own order put X
+//   after the fill, which made the register waits take the next chunk's fill too: 0.4 us
+//   at M = 16).
 // * v_mfma_f32_16x16x32_bf16 with W's fragment first; the 8 waves' partial sums of a block
 //   meet in LDS (double-buffered by block parity), and wave 0 sums, applies the epilogue and
-//   stores after the next chunk's barrier, under the other waves' MFMAs.
-template <int CPB>
+//   stores after the next chunk's barrier, under the other waves' MFMAs. The epilogue's
+//   common form (a bf16 bias, an activation) reads its bias with one LDS read a lane; a
+//   wait it had on a tile operand's direct load, and element-by-element vector reads,
+//   cost 0.6-0.9 us a call with a bias before.
+// The stream kernel's epilogue forms: kStreamEpFast -- an activation of acc times broadcast
+// scales (or none) plus an optional bf16 bias of unit stride, 4-byte aligned, N even --
+// reads its bias with one 8-byte LDS read a lane; kStreamEpGeneric reads every vector
+// operand element by element in any dtype and stride.
+constexpr int kStreamEpFast = 0;
+constexpr int kStreamEpGeneric = 1;
+
+template <int CPB, int EPF>
 __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   constexpr int NW = 8;
   constexpr int CH = 16 * 2048;  // a chunk: 16 rows x 2 KB
@@ -199,8 +213,16 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const int nb = (p.N + 15) / 16;
   const int G = gridDim.x;
   if ((int)blockIdx.x >= nb) return;
-  const int my_blocks = (nb - (int)blockIdx.x + G - 1) / G;
+  // a workgroup's blocks are consecutive (blocks [bstart, bstart + my_blocks)), and it
+  // walks each block's K chunks starting from chunk blockIdx.x % cpb, so the workgroups'
+  // first reads of X spread over its chunks (measured 0.3-0.6 us faster at M = 16 than
+  // blocks strided by the grid and every workgroup starting on chunk 0)
+  const int bstart = (int)(((int64_t)blockIdx.x * nb) / G);
+  const int my_blocks = (int)((((int64_t)blockIdx.x + 1) * nb) / G) - bstart;
+  auto block_of = [&](int j) { return bstart + j; };
   const int cpb = CPB ? CPB : p.g_total / 8;  // chunks a block
+  const int rot = (int)blockIdx.x % cpb;
+  auto kchunk = [&](int c) { const int r = c + rot; return r >= cpb ? r - cpb : r; };
   const int nq = my_blocks * cpb;             // chunks of this workgroup
 
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
@@ -222,8 +244,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   }
   auto fill = [&](int q) {
     if (q >= nq) return;  // past the end: nothing (the waits count what was issued)
-    const int jb = q / cpb, kc = q - jb * cpb;
-    const int bi = (int)blockIdx.x + jb * G;
+    const int jb = q / cpb, kc = kchunk(q - jb * cpb);
+    const int bi = block_of(jb);
     const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u);
     uint8_t* slot = ring + (q & (NR - 1)) * CH;
 #pragma unroll
@@ -247,8 +269,15 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
   auto ep_load = [&](int j) {
     if (wave != 0 || !(cs_vec || rs_vec || ra_vec)) return;
-    const int bi = (int)blockIdx.x + j * G;
+    const int bi = block_of(j);
     uint8_t* base = ring + EPV + (j % 3) * 768;
+    if constexpr (EPF == kStreamEpFast) {
+      // the block's 16 bf16 bias values: 8 lanes of one dword each, contiguous in LDS
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          make_rsrc(e.ra.p, (uint32_t)p.N * 2u), (__attribute__((address_space(3))) void*)(base + 512), 4,
+          lane < 8 ? (uint32_t)(bi * 32 + 4 * lane) : 0x7fffffffu, 0, 0, 0);
+      return;
+    }
     const int l = lane;
     constexpr uint32_t kOut = 0x7fffffffu;  // past every buffer's end: reads nothing
     // the word of element idx, from the operand's address rounded down to 4 bytes (the
@@ -297,7 +326,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   };
   // block j of this workgroup: its partial sums are at parity j & 1
   auto finish = [&](int j) {
-    const int bi = (int)blockIdx.x + j * G;
+    const int bi = block_of(j);
     i32x4 part[NW];
 #pragma unroll
     for (int w2 = 0; w2 < NW; ++w2) part[w2] = ds_read16(RED + (((j & 1) * NW + w2) * 64 + lane) * 16);
@@ -305,15 +334,21 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) sum += __builtin_bit_cast(f32x4, part[w2]);
     const int m = rf, n = bi * 16 + 4 * kq;
-    if (fused) {
+    if (EPF == kStreamEpFast && fused) {
+      const uint8_t* eo = ring + EPV + (j % 3) * 768;
+      const f32x4 ra = ra_vec ? unpack_bf16x4(*(const u32x2*)(eo + 512 + 8 * kq))
+                              : f32x4{ra_sc, ra_sc, ra_sc, ra_sc};
+      const float sc = cs_sc * rs_sc;
+      sum = act4(e.act, sum * f32x4{sc, sc, sc, sc} + ra + e.cadd);
+    } else if (fused) {
       const uint32_t* eo = (const uint32_t*)(ring + EPV + (j % 3) * 768);
       const float cs = cs_vec ? word_val(eo[m], e.cs.dt, hi_half(e.cs, (int64_t)m * e.cs.ld)) * e.cmul
                               : cs_sc;
       const f32x4 rs = rs_vec ? vec4(eo + 64 + 4 * kq, e.rs, n) : f32x4{rs_sc, rs_sc, rs_sc, rs_sc};
       const f32x4 ra = ra_vec ? vec4(eo + 128 + 4 * kq, e.ra, n) : f32x4{ra_sc, ra_sc, ra_sc, ra_sc};
-      sum = sum * (rs * cs) + ra;
-      if (e.ta.p && m < p.M && n < p.N) sum += ld_tile(e.ta, m, n);
-      sum = act4(e.act, sum + e.cadd);
+      // (no tile operand here: stream_takes leaves those calls to decode_kernel, since its
+      // direct load would make wave 0 wait for every fill in flight)
+      sum = act4(e.act, sum * (rs * cs) + ra + e.cadd);
     }
     if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
   };
@@ -327,12 +362,18 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // of q + 3 takes: in issue order the loads after x(q) and f(q) are f(q + 1), x(q + 1) and
   // f(q + 2), each 4 a wave where it exists (anything issued later only makes the wait
   // stricter); lgkmcnt(0) as well
-  auto wait_chunk = [&](int q) {
-    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq) + has_x(q + 1));
-    if (n >= 12) __builtin_amdgcn_s_waitcnt(wait_vm_dec(12) & ~(15 << 8));
-    else if (n == 8) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
-    else if (n == 4) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
-    else __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
+  // wave 0's epilogue-vector DMAs of the step before (ep_load) are among them too
+  const int nvec = EPF == kStreamEpFast ? (int)ra_vec : (int)cs_vec + (int)rs_vec + (int)ra_vec;
+  auto wait_chunk = [&](int q, bool ep_before) {
+    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq) + has_x(q + 1)) + (ep_before && wave == 0 ? nvec : 0);
+    switch (n) {
+#define HKX_WAIT_CASE(N) case N: __builtin_amdgcn_s_waitcnt(wait_vm_dec(N) & ~(15 << 8)); break;
+      HKX_WAIT_CASE(1) HKX_WAIT_CASE(2) HKX_WAIT_CASE(3) HKX_WAIT_CASE(4) HKX_WAIT_CASE(5)
+      HKX_WAIT_CASE(6) HKX_WAIT_CASE(7) HKX_WAIT_CASE(8) HKX_WAIT_CASE(9) HKX_WAIT_CASE(10)
+      HKX_WAIT_CASE(11) HKX_WAIT_CASE(12) HKX_WAIT_CASE(13) HKX_WAIT_CASE(14) HKX_WAIT_CASE(15)
+#undef HKX_WAIT_CASE
+      default: __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8)); break;
+    }
   };
   auto block_done = [&](int j) {
     ds_write16(RED + (((j & 1) * NW + wave) * 64 + lane) * 16, __builtin_bit_cast(i32x4, acc));
@@ -343,7 +384,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   auto xload = [&](int c, i32x4 (&dst)[4]) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      dst[s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * c + wave) * 256u);
+      dst[s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * kchunk(c) + wave) * 256u);
   };
 
   if constexpr (CPB > 0) {
@@ -352,18 +393,22 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     i32x4 x[CPB][4];
     ep_load(0);
     xload(0, x[0]);
+    __builtin_amdgcn_sched_barrier(0);
     fill(0);
     if (CPB > 1) xload(1, x[CPB > 1 ? 1 : 0]);
+    __builtin_amdgcn_sched_barrier(0);
     fill(1);
     fill(2);
     for (int j = 0; j < my_blocks; ++j) {
 #pragma unroll
       for (int c = 0; c < CPB; ++c) {
         const int q = j * CPB + c;
-        wait_chunk(q);
+        // the step before issued ep_load(j) when it was the first chunk of block j - 1
+        wait_chunk(q, (CPB == 1 ? c == 0 && j >= 1 : c == 1) && (CPB == 1 || j + 1 < my_blocks));
         __builtin_amdgcn_s_barrier();
         if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);  // older than the fills of q + 3 on
         if (c + 2 < CPB && j == 0) xload(c + 2, x[c + 2 < CPB ? c + 2 : 0]);
+        __builtin_amdgcn_sched_barrier(0);  // X before the fill: the waits count in that order
         fill(q + 3);
         if (c == 0 && j > 0 && wave == 0) finish(j - 1);
         mma(q, x[c]);
@@ -385,7 +430,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     fill(2);
     auto step = [&](int q, const i32x4 (&xc)[4], i32x4 (&xn)[4]) {
       const int j = q / cpb, c = q - j * cpb;
-      wait_chunk(q);
+      wait_chunk(q, c == 1 && j + 1 < my_blocks);
       __builtin_amdgcn_s_barrier();
       if (c == 0 && j + 1 < my_blocks) ep_load(j + 1);
       xnext(q + 2, xn);
