@@ -43,13 +43,15 @@ def _time(fn, reps=5):
 
 
 def mfma_tflops(fp8: bool = False, device="cuda:0") -> float:
-    """Dense MFMA TFLOP/s of 4 independent 32x32 chains a wave, 4 waves a CU x 256 CUs
-    (bf16 v_mfma_f32_32x32x16_bf16, fp8 v_mfma_f32_32x32x64_f8f6f4)."""
+    """Dense MFMA TFLOP/s of 4 independent 32x32 chains a wave, 8 waves a CU (two a SIMD)
+    x 256 CUs (bf16 v_mfma_f32_32x32x16_bf16, fp8 v_mfma_f32_32x32x64_f8f6f4). One wave a
+    SIMD leaves a gap between a wave's back-to-back bf16 MFMAs (measured 2.07-2.14
+    PFLOP/s against 2.47 with two, at 2.37 GHz); fp8's longer MFMA hides it either way."""
     import torch  # noqa: PLC0415
 
     L = _lib()
     cus = torch.cuda.get_device_properties(device).multi_processor_count
-    blocks, iters = cus * 4, 4000
+    blocks, iters = cus * 8, 4000
     out = torch.zeros(blocks, device=device)
     st = torch.cuda.current_stream(device).cuda_stream
     t = _time(lambda: L.hkxp_mfma(int(fp8), blocks, iters, ctypes.c_void_p(out.data_ptr()),
