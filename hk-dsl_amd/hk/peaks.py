@@ -21,16 +21,22 @@ def _lib():
         if not path.is_file():
             raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
         _LIB = ctypes.CDLL(str(path))
-        for f in ("hkxp_mfma", "hkxp_read", "hkxp_clock", "hkxp_lds"):
+        for f in ("hkxp_mfma", "hkxp_mfma_issue", "hkxp_read", "hkxp_clock", "hkxp_lds"):
             getattr(_LIB, f).restype = ctypes.c_int
     return _LIB
 
 
-def _time(fn, reps=5):
+def _time(fn, reps=10, warm_s=0.2):
+    """The best of `reps` launches of `fn`, after `warm_s` seconds of untimed launches: the
+    clocks take tens of milliseconds of load to settle."""
+    import time  # noqa: PLC0415
+
     import torch  # noqa: PLC0415
 
-    fn()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_s:
+        fn()
+        torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     best = float("inf")
     for _ in range(reps):
@@ -58,6 +64,23 @@ def mfma_tflops(fp8: bool = False, device="cuda:0") -> float:
                                   ctypes.c_void_p(st)))
     flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
     return blocks * 4 * iters * 4 * flops_per / t / 1e12
+
+
+def mfma_issue_tflops(waves_per_simd: int = 1, device="cuda:0") -> float:
+    """bf16 TFLOP/s of v_mfma_f32_16x16x32_bf16 (the GEMM kernels' instruction) issued back
+    to back, 8 independent chains a wave, `waves_per_simd` waves on each SIMD. One wave a
+    SIMD is the ceiling of a ping-pong schedule, where one wave of a SIMD issues the MFMAs
+    of a phase while the other reads LDS and fills."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks, iters = cus * 4 * waves_per_simd, 4000
+    out = torch.zeros(blocks, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    t = _time(lambda: L.hkxp_mfma_issue(blocks, iters, ctypes.c_void_p(out.data_ptr()),
+                                        ctypes.c_void_p(st)))
+    return blocks * 4 * iters * 8 * (2 * 16 * 16 * 32) / t / 1e12
 
 
 def hbm_read_gbs(nbytes: int = 2 << 30, device="cuda:0") -> float:
@@ -110,6 +133,8 @@ def lds_read_bytes_per_clk(pattern: int = 0, device="cuda:0") -> float:
 
 def measure(device="cuda:0") -> dict:
     return {"mfma_bf16_tflops": mfma_tflops(False, device),
+            "mfma_16x16x32_bf16_one_wave_a_simd_tflops": mfma_issue_tflops(1, device),
+            "mfma_16x16x32_bf16_two_waves_a_simd_tflops": mfma_issue_tflops(2, device),
             "mfma_fp8_tflops": mfma_tflops(True, device),
             "hbm_read_gbs": hbm_read_gbs(device=device),
             "shader_clock_ghz_mfma_load": shader_clock_ghz(device),

@@ -37,6 +37,31 @@ __global__ void __launch_bounds__(256) mfma_loop(float* out, int iters) {
   if (s == 1234.5f) out[blockIdx.x] = s;  // keeps the loop alive
 }
 
+// The GEMM kernels' instruction, v_mfma_f32_16x16x32_bf16, issued back to back by every
+// wave: CH independent 16x16 accumulators a wave. Written as inline asm so the compiler
+// keeps the accumulators in place (its own code for this loop shuffles them between
+// register files every iteration). With one wave a SIMD this is the rate of a schedule
+// whose MFMAs come from one wave at a time (the ping-pong GEMMs' math phases).
+template <int CH>
+__global__ void __launch_bounds__(256) mfma_issue_loop(float* out, int iters) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  f32x4v acc[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) acc[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const int l = threadIdx.x;
+  bf16x8 a = {(__bf16)(l * 1e-3f), (__bf16)1.f, (__bf16)0.5f, (__bf16)0.25f, (__bf16)1.f,
+              (__bf16)2.f, (__bf16)3.f, (__bf16)4.f};
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[j]) : "v"(a), "v"(a));
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) s += acc[j][0];
+  if (s == 1234.5f) out[blockIdx.x] = s;
+}
+
 __global__ void __launch_bounds__(256) read_kernel(const i32x4* p, size_t n16, int* out) {
   i32x4 acc = {0, 0, 0, 0};
   const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -110,6 +135,11 @@ int hkxp_lds(int pattern, int blocks, int iters, float* out, void* stream) {
 
 int hkxp_mfma16(int blocks, int iters, float* out, void* stream) {
   hipLaunchKernelGGL((mfma_loop<false, 16>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
+
+int hkxp_mfma_issue(int blocks, int iters, float* out, void* stream) {
+  hipLaunchKernelGGL((mfma_issue_loop<8>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
   return (int)hipGetLastError();
 }
 
