@@ -288,27 +288,42 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       // run g of a fragment's 16 values; runs 2 t and 2 t + 1 trade halves
       // (v_permlane32_swap), so lane l stores columns 16 t + 8 h + [0, 8)
       const int rf = lane & 31, h = lane >> 5;
+      // the row scales of this lane's four rows, read once; a column run's scales and bias
+      // are read once for the four row fragments that share them (one LDS wait a run,
+      // where a wait before every store left the epilogue on LDS latency)
+      [[maybe_unused]] float cs[2][2];
+      if constexpr (deq) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+          for (int f = 0; f < 2; ++f) cs[i][f] = ((const float*)ev)[128 * i + 64 * grp + 32 * f + rf];
+      }
 #pragma unroll
-          for (int f = 0; f < 2; ++f) {
-            const int ml = 128 * i + 64 * grp + 32 * f + rf;
-            [[maybe_unused]] const float cs = deq ? ((const float*)ev)[ml] : 1.0f;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              __builtin_amdgcn_sched_barrier(0);
-              const int c0 = 128 * j + 32 * wc + 16 * t;
+        for (int t = 0; t < 2; ++t) {
+          __builtin_amdgcn_sched_barrier(0);
+          const int c0 = 128 * j + 32 * wc + 16 * t;
+          [[maybe_unused]] f32x4 rs[2], bv[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int col = c0 + 8 * u + 4 * h;
+            if constexpr (deq) rs[u] = *(const f32x4*)(ev + 1024 + col * 4);
+            if constexpr (bias) bv[u] = unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
+          }
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+              const int ml = 128 * i + 64 * grp + 32 * f + rf;
               f32x4 v[2];
 #pragma unroll
               for (int u = 0; u < 2; ++u) {
                 const Acc& a = acc[i][j][f][0];
                 const int r = 8 * t + 4 * u;
                 v[u] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
-                const int col = c0 + 8 * u + 4 * h;
-                if constexpr (deq) v[u] = v[u] * (*(const f32x4*)(ev + 1024 + col * 4) * cs);
-                if constexpr (bias) v[u] += unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
+                if constexpr (deq) v[u] = v[u] * (rs[u] * cs[i][f]);
+                if constexpr (bias) v[u] += bv[u];
               }
               const u32x2 w0 = pack4<2>(HKX_BF16, v[0]), w1 = pack4<2>(HKX_BF16, v[1]);
               uint32_t x0 = w0.x, x1 = w1.x, y0 = w0.y, y1 = w1.y;
@@ -320,7 +335,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                     i32x4{(int)x0, (int)y0, (int)x1, (int)y1}, rc,
                     (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u, 0, 0);
             }
-          }
+        }
     } else {
     const int rf = lane & 15, q = lane >> 4;
     [[maybe_unused]] f32x4 bv[2][2];
