@@ -214,14 +214,16 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const int G = gridDim.x;
   if ((int)blockIdx.x >= nb) return;
   // a workgroup's blocks are consecutive (blocks [bstart, bstart + my_blocks)), and it
-  // walks each block's K chunks starting from chunk blockIdx.x % cpb, so the workgroups'
-  // first reads of X spread over its chunks (measured 0.3-0.6 us faster at M = 16 than
-  // blocks strided by the grid and every workgroup starting on chunk 0)
+  // walks each block's K chunks starting from chunk (blockIdx.x / 8) % cpb, so the first
+  // reads of X by the CUs of one XCD (workgroups blockIdx.x, + 8, + 16, ...) spread over
+  // its chunks (measured 0.3-0.6 us faster at M = 16 than blocks strided by the grid and
+  // every workgroup starting on chunk 0, and 0.1-0.2 us faster than a rotation by
+  // blockIdx.x % cpb, which starts all the CUs of an XCD on one chunk)
   const int bstart = (int)(((int64_t)blockIdx.x * nb) / G);
   const int my_blocks = (int)((((int64_t)blockIdx.x + 1) * nb) / G) - bstart;
   auto block_of = [&](int j) { return bstart + j; };
   const int cpb = CPB ? CPB : p.g_total / 8;  // chunks a block
-  const int rot = (int)blockIdx.x % cpb;
+  const int rot = ((int)blockIdx.x >> 3) % cpb;
   auto kchunk = [&](int c) { const int r = c + rot; return r >= cpb ? r - cpb : r; };
   const int nq = my_blocks * cpb;             // chunks of this workgroup
 
