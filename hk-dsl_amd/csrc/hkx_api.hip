@@ -39,6 +39,9 @@ int elem_bytes(int dt) {
     case HKX_FP16: return 2;
     case HKX_FP32: return 4;
     case HKX_FP8E4M3:
+    case HKX_FP8E5M2:
+    case HKX_FP8_E4M3_E5M2:
+    case HKX_FP8_E5M2_E4M3:
     case HKX_INT8: return 1;
     default: return 0;
   }
@@ -81,6 +84,21 @@ int wave_rows(int bm, int bn) {  // waves along M for a tile shape
 
 // The choice hkx_gemm makes for HKX_KERNEL_AUTO; the Python layer (hk.ops.gemm_cdna.route)
 // normally passes an explicit one.
+bool e5m2_pair(int dt) {
+  return dt == HKX_FP8E5M2 || dt == HKX_FP8_E4M3_E5M2 || dt == HKX_FP8_E5M2_E4M3;
+}
+
+// The tile kernels' operand-format code (TileArgs::ab_fmt) of an ab_dtype.
+int fmt_of(int dt) {
+  switch (dt) {
+    case HKX_FP8E4M3: return 1;
+    case HKX_FP8E5M2: return 2;
+    case HKX_FP8_E4M3_E5M2: return 3;
+    case HKX_FP8_E5M2_E4M3: return 4;
+    default: return 0;
+  }
+}
+
 void auto_choose(const HkxGemmArgs* a, int* kernel, int* bm, int* bn, int* splits) {
   const int m = a->m, n = a->n;
   const bool pair = a->ep.form == HKX_EP_SILU_MUL;
@@ -174,10 +192,11 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   if (!a->a || !a->b || !a->c) return fail(HKX_ERR_ARG, "A, B and C must be device pointers");
   if (a->m < 1 || a->k < 1 || a->n < 1)
     return fail(HKX_ERR_SHAPE, "M=%d, N=%d, K=%d; nothing to multiply", a->m, a->n, a->k);
-  if (a->ab_dtype != HKX_BF16 && a->ab_dtype != HKX_FP8E4M3)
-    return fail(HKX_ERR_DTYPE, "A and B are bf16 or fp8-e4m3 (dtype %d)", a->ab_dtype);
+  if (a->ab_dtype != HKX_BF16 && a->ab_dtype != HKX_FP8E4M3 && !e5m2_pair(a->ab_dtype))
+    return fail(HKX_ERR_DTYPE, "A and B are bf16, fp8-e4m3 or an e5m2 pair (dtype %d)",
+                a->ab_dtype);
   const int ob = elem_bytes(a->c_dtype);
-  if (!ob) return fail(HKX_ERR_DTYPE, "C dtype %d", a->c_dtype);
+  if (!ob || a->c_dtype > HKX_INT8) return fail(HKX_ERR_DTYPE, "C dtype %d", a->c_dtype);
   const int eb = elem_bytes(a->ab_dtype);
   const int kstep = 128 / eb;
   if (a->k % kstep || a->n % 4)
@@ -201,6 +220,11 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   int kernel = a->kernel, bm = a->tile_m, bn = a->tile_n, splits = a->splits;
   if (kernel == HKX_KERNEL_AUTO) auto_choose(a, &kernel, &bm, &bn, &splits);
   if (splits < 1) splits = 1;
+  if (e5m2_pair(a->ab_dtype) &&
+      (kernel != HKX_KERNEL_TILE || bm != 256 || bn != 256 ||
+       (a->tile_schedule != HKX_TILE_RING && a->tile_schedule != HKX_TILE_AUTO) || a->variant))
+    return fail(HKX_ERR_ARG, "e5m2 operands run on the 256x256 ring tile kernel "
+                "(kernel TILE, tile 256x256, schedule ring or auto, variant 0)");
   p->kernel = kernel;
   p->pair = pair;
   if (kernel == HKX_KERNEL_TILE) {
@@ -352,6 +376,11 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
   // The ring kernel: one workgroup a CU (a split's share of them) walking its tiles. A call
   // it does not take (an unaligned C, N % 8 != 0, a strided 16-bit column scale) runs on
   // the ping-pong kernel, which takes every 256 x 256 call.
+  if (t.ab_fmt > 1) {  // e5m2 pairs: the ring kernel only (make_plan and hkx_gemm checked)
+    dim3 g = grid;
+    g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
+    return hkx::launch_ring(t, fp8, mode, g, s);
+  }
   if (p.schedule == HKX_TILE_RING && hkx::ring_takes(t, fp8, mode)) {
     dim3 g = grid;
     g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
@@ -446,7 +475,7 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
   if (rc) return rc;
   const HkxGemmArgs& a = *args;
   hipStream_t s = (hipStream_t)stream;
-  const bool fp8 = a.ab_dtype == HKX_FP8E4M3;
+  const bool fp8 = a.ab_dtype != HKX_BF16;
   const int eb = elem_bytes(a.ab_dtype);
   const int ob = elem_bytes(a.c_dtype);
   const long long wcols = p.pair ? 2LL * a.n : a.n;
@@ -455,6 +484,7 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
 
   if (p.kernel == HKX_KERNEL_TILE) {
     hkx::TileArgs t{};
+    t.ab_fmt = fmt_of(a.ab_dtype);
     t.a = a.a;
     t.b = a.b;
     t.a_bytes = (uint32_t)((long long)a.m * a.lda * eb);
@@ -492,6 +522,9 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       else if (ob == 1) mode = hkx::kStore8;
       else mode = hkx::kStoreF32;
     }
+    if (t.ab_fmt > 1 && !hkx::ring_takes(t, fp8, mode))
+      return fail(HKX_ERR_SHAPE, "e5m2 operands run on the ring kernel, which needs C's rows "
+                  "16-byte aligned and N a multiple of 8");
     // The columns from c0 on as a call of their own: B's rows, C's columns and the
     // per-column epilogue operands (vectors and tiles; broadcasts stay) from column c0.
     auto from_col = [&](const hkx::TileArgs& t0, int c0) {

@@ -34,7 +34,9 @@ int quad_form(const TileArgs& a, bool fp8, int mode) {
 
 }  // namespace
 
-bool quad_takes(const TileArgs& a, bool fp8, int mode) { return quad_form(a, fp8, mode) >= 0; }
+bool quad_takes(const TileArgs& a, bool fp8, int mode) {
+  return a.ab_fmt <= 1 && quad_form(a, fp8, mode) >= 0;
+}
 
 #define HKX_QUAD(ACT, EPF) hipLaunchKernelGGL((quad_kernel<ACT, EPF>), grid, dim3(512), 0, s, a)
 #define HKX_QUAD_ACTS(EPF)                                            \

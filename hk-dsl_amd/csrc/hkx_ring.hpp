@@ -71,8 +71,13 @@ constexpr int kEpDeq = 2;      // act(acc cs[m] rs[n]), cs and rs fp32
 constexpr int kEpDeqBias = 3;  // act(acc cs[m] rs[n] + ra[n]), cs and rs fp32, ra bf16
 constexpr int kEpGeneric = 4;  // the whole fused form with run-time types and output type
 
-template <bool FP8, int MODE, int ACT, int EPF, bool MX = false>
+// FP8: 0 bf16 operands; 1 fp8 e4m3 x e4m3; 2 e5m2 x e5m2; 3 A e4m3 x B e5m2; 4 A e5m2 x B
+// e4m3 (TileArgs::ab_fmt). The scaled MFMA takes its first operand's format (here B's, as
+// B's fragment goes first) in cbsz and its second's (A's) in blgp: 0 e4m3, 1 e5m2.
+template <int FP8, int MODE, int ACT, int EPF, bool MX = false>
 __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
+  constexpr int FMT_B = (FP8 == 2 || FP8 == 3) ? 1 : 0;
+  constexpr int FMT_A = (FP8 == 2 || FP8 == 4) ? 1 : 0;
   constexpr int BM = 256, BN = 256;
   constexpr int FR = FP8 ? 32 : 16;           // fragment edge
   constexpr int FM = 64 / FR, FN = 128 / FR;  // fragments of a wave's 64 x 128
@@ -88,8 +93,8 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
   constexpr int OUTW = PAIR ? BN / 2 : BN;
   static_assert(!(PAIR && FP8) && !(MODE == kStore8 && PAIR), "modes");
   static_assert(SMEM <= 160 * 1024, "LDS");
-  using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
-  using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
+  using Frag = typename std::conditional<FP8 != 0, i32x8, bf16x8>::type;
+  using Acc = typename std::conditional<FP8 != 0, f32x16, f32x4>::type;
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
@@ -312,8 +317,8 @@ __global__ void __launch_bounds__(512, 1) ring_kernel(const TileArgs p) {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, 0, 0, 0,
                                                                      (int)sfb[j], 0, (int)sfa[i]);
         else if constexpr (FP8)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, 0, 0, 0, 0,
-                                                                     0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, FMT_B,
+                                                                     FMT_A, 0, 0, 0, 0);
         else
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], c, 0, 0, 0);
       }

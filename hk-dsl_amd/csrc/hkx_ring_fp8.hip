@@ -6,8 +6,27 @@ namespace hkx {
 
 #define HKX_RING(MODE, ACT, EPF) hipLaunchKernelGGL((ring_kernel<true, MODE, ACT, EPF>), grid, block, 0, s, a)
 
+#define HKX_RING_FMT(FMT, MODE) hipLaunchKernelGGL((ring_kernel<FMT, MODE, -1, kEpGeneric>), grid, block, 0, s, a)
+
+// e5m2 pairs: the generic epilogue form, into a 16-bit C, an 8-bit C or fp32 (C or split
+// shares)
+template <int FMT>
+static hipError_t launch_fmt(const TileArgs& a, int mode, dim3 grid, hipStream_t s) {
+  const dim3 block(512);
+  switch (mode) {
+    case kStore16: HKX_RING_FMT(FMT, kStore16); break;
+    case kStore8: HKX_RING_FMT(FMT, kStore8); break;
+    case kStoreF32: HKX_RING_FMT(FMT, kStoreF32); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s) {
   const dim3 block(512);
+  if (a.ab_fmt == 2) return launch_fmt<2>(a, mode, grid, s);
+  if (a.ab_fmt == 3) return launch_fmt<3>(a, mode, grid, s);
+  if (a.ab_fmt == 4) return launch_fmt<4>(a, mode, grid, s);
   switch (mode) {
     case kStore16:
       if (epf == kEpNone && act == HKX_ACT_NONE) HKX_RING(kStore16, HKX_ACT_NONE, kEpNone);

@@ -54,6 +54,9 @@ struct TileArgs {
   const uint8_t* sb;
   uint32_t sa_ld, sb_ld;
   uint32_t sa_bytes, sb_bytes;
+  // fp8 operand formats: 1 e4m3 x e4m3, 2 e5m2 x e5m2, 3 A e4m3 x B e5m2, 4 A e5m2 x B e4m3
+  // (0 for bf16); formats past 1 run on the ring kernel only
+  int32_t ab_fmt;
 };
 
 // How a tile leaves the kernel.

@@ -23,6 +23,8 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhkx.so"
 # ---- constants of include/hkx.h
 OK, ERR_SHAPE, ERR_DTYPE, ERR_WORKSPACE, ERR_LAUNCH, ERR_ARG = range(6)
 BF16, FP16, FP32, FP8E4M3, INT8 = range(5)
+#: ab_dtype codes of fp8 operand pairs with e5m2: both, A e4m3 x B e5m2, A e5m2 x B e4m3
+FP8E5M2, FP8_E4M3_E5M2, FP8_E5M2_E4M3 = 5, 6, 7
 ROW, COL, TILE = 1, 2, 3
 EP_NONE, EP_FUSED, EP_PROGRAM, EP_SILU_MUL = range(4)
 ACT_NONE, ACT_GELU_TANH, ACT_SILU, ACT_RELU = range(4)
@@ -149,7 +151,7 @@ def dtype_code(dt) -> int:
     import torch  # noqa: PLC0415
 
     m = {torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32,
-         torch.float8_e4m3fn: FP8E4M3, torch.int8: INT8}
+         torch.float8_e4m3fn: FP8E4M3, torch.int8: INT8, torch.float8_e5m2: FP8E5M2}
     if dt not in m:
         raise TypeError(f"hk: {dt} is not an element type the kernels take")
     return m[dt]

@@ -68,6 +68,11 @@ extern "C" {
 #define HKX_FP32 2
 #define HKX_FP8E4M3 3 /* OCP e4m3 (float8_e4m3fn): max 448, no inf */
 #define HKX_INT8 4
+/* fp8 operand pairs with e5m2 (OCP float8_e5m2: max 57344, inf and nan), as ab_dtype only;
+ * they run on the 256 x 256 ring tile kernel: */
+#define HKX_FP8E5M2 5        /* A and B e5m2 */
+#define HKX_FP8_E4M3_E5M2 6  /* A e4m3, B e5m2 (e.g. activations against a gradient) */
+#define HKX_FP8_E5M2_E4M3 7  /* A e5m2, B e4m3 */
 
 /* Epilogue operand kinds: what an operand is against C (M, N) -- templates/gemm.py:116-135. */
 #define HKX_ROW 1  /* (N,) or (1, N): one value per column of C (a bias, a per-channel scale) */
@@ -196,7 +201,7 @@ typedef struct HkxGemmArgs {
   void* c;       /* (M, N), row stride ldc elements */
   int64_t lda, ldb, ldc;
   int32_t m, n, k;
-  int32_t ab_dtype; /* HKX_BF16 or HKX_FP8E4M3 (both operands) */
+  int32_t ab_dtype; /* HKX_BF16, HKX_FP8E4M3 (both operands), or an e5m2 pair code */
   int32_t c_dtype;  /* HKX_BF16 / HKX_FP16 / HKX_FP32 / HKX_INT8 / HKX_FP8E4M3 */
   int32_t kernel;   /* HKX_KERNEL_* */
   int32_t tile_m;   /* TILE: 64, 128 or 256 */

@@ -305,3 +305,27 @@ def test_workspace_used_under_capture_is_never_freed(monkeypatch):
     assert nat.workspace("cpu", 32) is small
     nat.workspace("cpu", 4096)
     assert nat._PINNED == []
+
+
+def test_scaled_mm_argument_errors_on_the_cpu():
+    """scaled_mm refuses what the reference refuses before any launch
+    (python/hk/ops/gemm.py:911-966): a non-fp8 operand, a bias with an fp32 out, and
+    accumulate=True without an fp32 out."""
+    import torch
+
+    import hk
+
+    a8 = torch.zeros(4, 128, dtype=torch.float8_e5m2)
+    b8 = torch.zeros(8, 128, dtype=torch.float8_e4m3fn)
+    with pytest.raises(TypeError, match="float8_e4m3fn or float8_e5m2"):
+        hk.ops.scaled_mm(a8.half(), b8, 1.0, 1.0)
+    with pytest.raises(ValueError, match="fp32 out takes no bias"):
+        hk.ops.scaled_mm(a8, b8, 1.0, 1.0, bias=torch.zeros(8), out=torch.zeros(4, 8))
+    with pytest.raises(ValueError, match="accumulate=True"):
+        hk.ops.scaled_mm(a8, b8, 1.0, 1.0, accumulate=True)
+    from hk import _native as nat
+    from hk.ops import gemm as G
+
+    assert G._pair_code(a8, b8) == nat.FP8_E5M2_E4M3
+    assert G._pair_code(b8, a8) == nat.FP8_E4M3_E5M2
+    assert G._pair_code(a8, a8) == nat.FP8E5M2 and G._pair_code(b8, b8) == nat.FP8E4M3
