@@ -15,9 +15,9 @@ and this one keeps:
 * the op is `torch.ops.<ns>.<name>` with a fake for torch.compile, called without the
   dispatcher from eager code, its calls counted by path (captured calls apart);
 * a patch declares itself `graph="safe"` (capturable) or `graph="never"` (with the
-  reason); under capture a "never" patch raises `GraphCaptureError`, and an error a
-  "safe" patch meets because the stream is capturing becomes a `GraphCaptureError`
-  naming the patch.
+  reason); under capture a "never" patch raises `GraphCaptureError`, and a "safe" one runs
+  inside `no_host_sync`, where a host synchronisation raises a `GraphCaptureError` naming
+  the patch.
 
 The design here: a table is compiled, per shape, into a step function over M -- sorted
 breakpoints and the path holding from each breakpoint to the next, gaps already turned
@@ -28,9 +28,11 @@ through `torch.library.define` / `impl` / `register_fake`.
 from __future__ import annotations
 
 import bisect
+import contextlib
 import functools
 import json
 import os
+import warnings
 from pathlib import Path
 from typing import Callable, Dict, Iterable, List, Optional, Sequence, Tuple
 
@@ -62,6 +64,39 @@ def compiling() -> bool:
     except ImportError:
         return False
     return torch.compiler.is_compiling()
+
+
+def _names_a_sync(err: BaseException) -> bool:
+    text = str(err).lower()
+    return any(w in text for w in _CAPTURE_WORDS)
+
+
+@contextlib.contextmanager
+def no_host_sync(what: str):
+    """A block in which a host synchronisation is an error naming `what`: torch's sync
+    debug mode is raised to "error" for its duration (so a synchronising call raises
+    before it runs, rather than invalidating a capture or stalling a replay), and such an
+    error comes out as `GraphCaptureError`. The mode in force before is restored."""
+    import torch  # noqa: PLC0415
+
+    before = torch.cuda.get_sync_debug_mode()
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")     # torch warns when the mode is turned up
+        torch.cuda.set_sync_debug_mode("error")
+    try:
+        yield
+    except GraphCaptureError:
+        raise
+    except RuntimeError as err:
+        if not _names_a_sync(err):
+            raise
+        first = str(err).splitlines()[0] if str(err) else type(err).__name__
+        raise GraphCaptureError(
+            f"{what} synchronised with the host (or made a call a capture refuses) while a "
+            f"CUDA graph was being captured; a replay runs no Python, so anything read back "
+            f"would be frozen at capture time: {first}") from err
+    finally:
+        torch.cuda.set_sync_debug_mode(before)
 
 
 # ---------------------------------------------------------------- patches
@@ -108,19 +143,8 @@ class Patch:
             if not capturing():
                 return fn(*args, **kwargs)
             self._refuse_capture()
-            try:
+            with no_host_sync(self.name):
                 return fn(*args, **kwargs)
-            except GraphCaptureError:
-                raise
-            except RuntimeError as err:
-                text = str(err)
-                if not any(w in text.lower() for w in _CAPTURE_WORDS):
-                    raise
-                raise GraphCaptureError(
-                    f"{self.name} did something a captured graph cannot replay (a host "
-                    f"synchronisation or an unsupported call while the stream was "
-                    f"capturing): {text.splitlines()[0] if text else type(err).__name__}"
-                ) from err
 
         return held
 
@@ -360,4 +384,5 @@ def isolate_compile_cache(route: str) -> str:
 
 
 __all__ = ["Op", "Patch", "RouteTable", "GraphCaptureError", "capturing", "compiling",
+           "no_host_sync",
            "shipped_table", "isolate_compile_cache", "PATCHES"]

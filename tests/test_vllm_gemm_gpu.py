@@ -206,3 +206,27 @@ def test_it_replays_from_a_cuda_graph(op, m):
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
         _check(y, x2, w)
+
+
+def test_the_graph_contract_names_the_patch():
+    """Under CUDA-graph capture a graph-safe op that synchronises with the host raises
+    GraphCaptureError naming it (torch's sync debug mode refuses the sync before it runs,
+    so the capture itself stays valid), and a graph="never" op refuses to run at all."""
+    from hk.integration import engine
+
+    syncs = engine.Op("hk_test::syncs", "syncs(Tensor x) -> Tensor", lambda x: torch.empty_like(x),
+                      paths=("a",))
+    syncs.define(lambda x: x * x.sum().item())
+    never = engine.Op("hk_test::never", "never(Tensor x) -> Tensor", lambda x: torch.empty_like(x),
+                      paths=("a",), graph="never", why="its route reads a host-side counter")
+    never.define(lambda x: x + 1)
+    x = torch.ones(8, device=DEV)
+    assert float(syncs(x)[0]) == 8.0 and float(never(x)[0]) == 2.0   # eager: fine
+    torch.cuda.synchronize()
+    for op, match in ((syncs, "hk_test::syncs synchronised"), (never, "reads a host-side")):
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(engine.GraphCaptureError, match=match):
+            with torch.cuda.graph(g):
+                op(x)
+        torch.cuda.synchronize()
+    assert float(syncs(x)[0]) == 8.0                                   # eager again
