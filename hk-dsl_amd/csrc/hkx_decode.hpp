@@ -381,12 +381,39 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     ds_write16(RED + (((j & 1) * NW + wave) * 64 + lane) * 16, __builtin_bit_cast(i32x4, acc));
     acc = f32x4{0.f, 0.f, 0.f, 0.f};
   };
-  // lane l's share of X for chunk c: row l % 16, 16 bytes at 16 (l / 16) + 64 s of K group
-  // 8 c + wave (chunk c's group of this wave), for k-steps s
+  // This wave's share of X for chunk c (K group 8 c + wave: 16 rows x 256 bytes) in four
+  // loads of whole 128-byte lines: load i brings rows 8 (i & 1) + [0, 8), line i >> 1 of
+  // the group, lane l row l / 8 and piece l % 8 of the line (consecutive lanes along a
+  // line). In the MFMA layout -- lane l holding row l % 16 -- a load asks for 64 bytes of
+  // 16 lines: measured 0.4-0.5 us slower at M = 16 (lines with the row in the low lane
+  // bits were no faster either).
   auto xload = [&](int c, i32x4 (&dst)[4]) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      dst[s] = buf_load16(rx, (uint32_t)rf * p.lda_b + kq * 16 + s * 64, (uint32_t)(8 * kchunk(c) + wave) * 256u);
+    for (int i = 0; i < 4; ++i)
+      dst[i] = buf_load16(rx, (uint32_t)((lane >> 3) + 8 * (i & 1)) * p.lda_b + (uint32_t)(lane & 7) * 16 + (i >> 1) * 128,
+                          (uint32_t)(8 * kchunk(c) + wave) * 256u);
+  };
+  // ... then into the MFMA layout, just before the chunk's MFMAs: k-step s = 2 h + e of lane
+  // (rf, kq) takes row rf, piece 4 s + kq of the group, which load 2 h + rf / 8 holds at
+  // lane 8 (rf % 8) + 4 e + kq. Loads 2 h (a) and 2 h + 1 (b) first trade 4-lane halves
+  // (DPP row shifts by 4): m0 keeps a's pieces 0-3 of each row in place with b's beside
+  // them (lanes 8 r + 4 + k), m1 a's pieces 4-7 in place with b's beside them (lanes
+  // 8 r + k); then one ds_bpermute a dword. (Two ds_bpermutes a dword and a select, or the
+  // shuffle moved off the path to the MFMAs, measured slower.)
+  const int xsrc0 = 4 * (8 * (rf & 7) + kq + 4 * (rf >> 3)), xsrc1 = 4 * (8 * (rf & 7) + kq + 4 * (rf < 8));
+  const bool hi4 = (lane & 4) != 0;
+  auto xperm = [&](i32x4 (&v)[4]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int a = v[2 * h][d], b = v[2 * h + 1][d];
+        const int bs = __builtin_amdgcn_update_dpp(0, b, 0x114, 0xf, 0xf, false);  // row_shr:4
+        const int bl = __builtin_amdgcn_update_dpp(0, b, 0x104, 0xf, 0xf, false);  // row_shl:4
+        const int m0 = hi4 ? bs : a, m1 = hi4 ? a : bl;
+        v[2 * h][d] = __builtin_amdgcn_ds_bpermute(xsrc0, m0);
+        v[2 * h + 1][d] = __builtin_amdgcn_ds_bpermute(xsrc1, m1);
+      }
   };
 
   if constexpr (CPB > 0) {
@@ -413,6 +440,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
         __builtin_amdgcn_sched_barrier(0);  // X before the fill: the waits count in that order
         fill(q + 3);
         if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+        if (j == 0) xperm(x[c]);  // (X is held in registers from the first block on)
         mma(q, x[c]);
       }
       block_done(j);
@@ -430,7 +458,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     xnext(1, xs[1]);
     fill(1);
     fill(2);
-    auto step = [&](int q, const i32x4 (&xc)[4], i32x4 (&xn)[4]) {
+    auto step = [&](int q, i32x4 (&xc)[4], i32x4 (&xn)[4]) {
       const int j = q / cpb, c = q - j * cpb;
       wait_chunk(q, c == 1 && j + 1 < my_blocks);
       __builtin_amdgcn_s_barrier();
@@ -438,6 +466,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       xnext(q + 2, xn);
       fill(q + 3);
       if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+      xperm(xc);
       mma(q, xc);
       if (c == cpb - 1) block_done(j);
     };
