@@ -201,6 +201,8 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
                      "peak_measured": peaks["mfma_bf16_tflops"],
                      "frac_measured": round(achieved / peaks["mfma_bf16_tflops"], 4),
+                     "peak_measured_random_operands": peaks["mfma_bf16_random_operands_tflops"],
+                     "frac_measured_random_operands": round(achieved / peaks["mfma_bf16_random_operands_tflops"], 4),
                      "kernel": kname,
                      "avg_launch_us": round(mean_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
                      "algorithmic_flops_per_launch": flops},
@@ -239,9 +241,12 @@ def measured_peaks():
 
     return {"mfma_bf16_tflops": round(peaks.mfma_tflops(False), 1),
             "mfma_fp8_tflops": round(peaks.mfma_tflops(True), 1),
+            "mfma_bf16_random_operands_tflops": round(peaks.mfma_random_tflops(False), 1),
+            "mfma_fp8_random_operands_tflops": round(peaks.mfma_random_tflops(True), 1),
             "hbm_read_gbs": round(peaks.hbm_read_gbs(), 1),
-            "how": "hk.peaks: register-only 32x32 MFMA loop on every CU; one pass of 16-byte "
-                   "non-temporal reads over 2 GiB"}
+            "how": "hk.peaks: register-only 32x32 MFMA loop on every CU, on constant operands "
+                   "and on random ones (the power-limited rate on data that toggles like real "
+                   "tensors); one pass of 16-byte non-temporal reads over 2 GiB"}
 
 
 def other_configs(steps, warmup, peaks):
@@ -262,6 +267,8 @@ def other_configs(steps, warmup, peaks):
         out[f"cfg3_gate_up_silu_mul_M{m}"] = {"TFLOP/s": round(fl / t / 1e12, 1),
                                               "frac_bf16_peak": round(fl / t / 1e12 / PEAK_BF16, 4),
                                               "frac_measured": round(fl / t / 1e12 / peaks["mfma_bf16_tflops"], 4),
+                                              "frac_measured_random_operands": round(
+                                                  fl / t / 1e12 / peaks["mfma_bf16_random_operands_tflops"], 4),
                                               "us": round(t * 1e6, 1)}
         del x, wt, y
     # config 4: decode, 4 weight copies (403 MB) rotated past the 256 MB MALL; kernel time
@@ -297,6 +304,8 @@ def other_configs(steps, warmup, peaks):
     out["cfg5_fp8_scaled_dequant_bias"] = {"TFLOP/s": round(fl / t / 1e12, 1),
                                            "frac_fp8_peak": round(fl / t / 1e12 / PEAK_FP8, 4),
                                            "frac_measured": round(fl / t / 1e12 / peaks["mfma_fp8_tflops"], 4),
+                                           "frac_measured_random_operands": round(
+                                               fl / t / 1e12 / peaks["mfma_fp8_random_operands_tflops"], 4),
                                            "us": round(t * 1e6, 1)}
     return out
 

@@ -21,7 +21,7 @@ def _lib():
         if not path.is_file():
             raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
         _LIB = ctypes.CDLL(str(path))
-        for f in ("hkxp_mfma", "hkxp_mfma_issue", "hkxp_read", "hkxp_clock", "hkxp_lds"):
+        for f in ("hkxp_mfma", "hkxp_mfma_rand", "hkxp_mfma_issue", "hkxp_read", "hkxp_clock", "hkxp_lds"):
             getattr(_LIB, f).restype = ctypes.c_int
     return _LIB
 
@@ -64,6 +64,25 @@ def mfma_tflops(fp8: bool = False, device="cuda:0") -> float:
                                   ctypes.c_void_p(st)))
     flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
     return blocks * 4 * iters * 4 * flops_per / t / 1e12
+
+
+def mfma_random_tflops(fp8: bool = False, device="cuda:0") -> float:
+    """mfma_tflops's loop on random operands (random sign and mantissa bits, four operand
+    sets rotated): the MFMA rate when the datapath toggles as on real tensors. Under the
+    board's power limit this runs at a lower clock than the constant-operand loop, so it is
+    the ceiling a GEMM on random data can reach with its MFMAs busy every cycle."""
+    import torch  # noqa: PLC0415
+
+    L = _lib()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks, iters = cus * 8, 1000
+    out = torch.zeros(blocks, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    t = _time(lambda: L.hkxp_mfma_rand(int(fp8), blocks, iters, ctypes.c_void_p(out.data_ptr()),
+                                       ctypes.c_void_p(st)), warm_s=0.5)
+    flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
+    # 4 waves a workgroup, 16 MFMAs a wave an iteration (4 operand sets x 4 accumulators)
+    return blocks * 4 * iters * 16 * flops_per / t / 1e12
 
 
 def mfma_issue_tflops(waves_per_simd: int = 1, device="cuda:0") -> float:
@@ -133,6 +152,8 @@ def lds_read_bytes_per_clk(pattern: int = 0, device="cuda:0") -> float:
 
 def measure(device="cuda:0") -> dict:
     return {"mfma_bf16_tflops": mfma_tflops(False, device),
+            "mfma_bf16_random_operands_tflops": mfma_random_tflops(False, device),
+            "mfma_fp8_random_operands_tflops": mfma_random_tflops(True, device),
             "mfma_16x16x32_bf16_one_wave_a_simd_tflops": mfma_issue_tflops(1, device),
             "mfma_16x16x32_bf16_two_waves_a_simd_tflops": mfma_issue_tflops(2, device),
             "mfma_fp8_tflops": mfma_tflops(True, device),

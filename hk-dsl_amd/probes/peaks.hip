@@ -37,6 +37,52 @@ __global__ void __launch_bounds__(256) mfma_loop(float* out, int iters) {
   if (s == 1234.5f) out[blockIdx.x] = s;  // keeps the loop alive
 }
 
+// The same loop on operands of random bits (bf16: random sign and mantissa, exponent in
+// [2^-7, 2^8); fp8 e4m3: random bytes with the exponent's top bit clear, so no NaN), four
+// operand sets rotated so that consecutive MFMAs see different data: the MFMA rate when
+// the datapath toggles as it does on real tensors, which draws more power than the
+// constant operands above and so runs at a lower clock under the board's power limit.
+__device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16; x *= 0x7feb352dU; x ^= x >> 15; x *= 0x846ca68bU; x ^= x >> 16;
+  return x;
+}
+template <bool FP8, int CH = 4>
+__global__ void __launch_bounds__(256) mfma_rand_loop(float* out, int iters) {
+  f32x16 acc[CH] = {};
+  const uint32_t seed = (uint32_t)(blockIdx.x * 256 + threadIdx.x) * 0x9E3779B9u;
+  i32x4 ab[8];   // bf16: 4 A and 4 B operand sets
+  i32x8 fb[8];   // fp8
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const uint32_t r = mix32(seed + 8 * u + d);
+      // bf16 pair: sign and mantissa random, exponent 120-135
+      const uint32_t h0 = (r & 0x807f) | ((120 + ((r >> 8) & 15)) << 7);
+      const uint32_t h1 = ((r >> 16) & 0x807f) | ((120 + ((r >> 24) & 15)) << 7);
+      if (d < 4) ab[u][d] = (int)(h0 | (h1 << 16));
+      fb[u][d] = (int)(r & 0xbfbfbfbfu);
+    }
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        if constexpr (FP8)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[u], fb[4 + ((u + j) & 3)], acc[j], 0, 0, 0,
+                                                                   0, 0, 0);
+        else
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ab[u]),
+                                                           __builtin_bit_cast(bf16x8, ab[4 + ((u + j) & 3)]),
+                                                           acc[j], 0, 0, 0);
+      }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) s += acc[j][0] + acc[j][15];
+  if (s == 1234.5f) out[blockIdx.x] = s;
+}
+
 // The GEMM kernels' instruction, v_mfma_f32_16x16x32_bf16, issued back to back by every
 // wave: CH independent 16x16 accumulators a wave. Written as inline asm so the compiler
 // keeps the accumulators in place (its own code for this loop shuffles them between
@@ -148,6 +194,14 @@ int hkxp_mfma(int fp8, int blocks, int iters, float* out, void* stream) {
     hipLaunchKernelGGL(mfma_loop<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
   else
     hipLaunchKernelGGL(mfma_loop<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
+
+int hkxp_mfma_rand(int fp8, int blocks, int iters, float* out, void* stream) {
+  if (fp8)
+    hipLaunchKernelGGL(mfma_rand_loop<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  else
+    hipLaunchKernelGGL(mfma_rand_loop<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
   return (int)hipGetLastError();
 }
 
