@@ -43,12 +43,6 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
   return launch_fn<16>(a, fn, mf, mode, grid, s);
 }
 
-bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
-  const int groups = a.g_total;  // 128-element K groups
-  const bool tile_operand = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
-  return splits == 1 && !pair && !tile_operand && a.M <= 16 && groups % 8 == 0 && groups <= 256;
-}
-
 // Whether the stream kernel's fast epilogue form takes the call's epilogue: no tile or
 // vector scales (broadcast ones are fine), a bias -- if any -- bf16 of unit stride, 4-byte
 // aligned, N even.
@@ -61,22 +55,36 @@ static bool stream_fast(const DecodeArgs& a) {
   return true;
 }
 
-template <int EPF>
+bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
+  const int groups = a.g_total;  // 128-element K groups
+  const bool tile_operand = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
+  // two 16-token fragments (M 17-32) keep one buffer of partial sums, which needs two chunks
+  // a block (K of 2048 and up)
+  return splits == 1 && !pair && !tile_operand && groups % 8 == 0 && groups <= 256 &&
+         (a.M <= 16 || (a.M <= 32 && groups >= 16));
+}
+
+template <int EPF, int MF>
 static hipError_t launch_stream_ep(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(512);
   switch (a.g_total / 8) {
-    case 1: hipLaunchKernelGGL((stream_kernel<1, EPF>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((stream_kernel<2, EPF>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((stream_kernel<3, EPF>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((stream_kernel<4, EPF>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((stream_kernel<0, EPF>), grid, block, 0, s, a); break;
+    case 1:
+      if constexpr (MF == 1) { hipLaunchKernelGGL((stream_kernel<1, EPF, MF>), grid, block, 0, s, a); break; }
+      return hipErrorInvalidValue;  // (stream_takes sends no such call)
+    case 2: hipLaunchKernelGGL((stream_kernel<2, EPF, MF>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((stream_kernel<3, EPF, MF>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((stream_kernel<4, EPF, MF>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((stream_kernel<0, EPF, MF>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  return stream_fast(a) ? launch_stream_ep<kStreamEpFast>(a, grid, s)
-                        : launch_stream_ep<kStreamEpGeneric>(a, grid, s);
+  if (a.M > 16)
+    return stream_fast(a) ? launch_stream_ep<kStreamEpFast, 2>(a, grid, s)
+                          : launch_stream_ep<kStreamEpGeneric, 2>(a, grid, s);
+  return stream_fast(a) ? launch_stream_ep<kStreamEpFast, 1>(a, grid, s)
+                        : launch_stream_ep<kStreamEpGeneric, 1>(a, grid, s);
 }
 
 }  // namespace hkx

@@ -164,7 +164,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 
 
 // The streaming decode GEMM: one workgroup a CU walks its share of the 16-row blocks of W
-// (a consecutive run of them), for M <= 16 (one 16-token fragment), unpaired, no split, K a multiple of
+// (a consecutive run of them), for M <= 32 (MF = 1 or 2 16-token fragments; two from K = 2048
+// up), unpaired, no split, K a multiple of
 // 1024: CPB chunks of 1024 a block (CPB = 1..4), or, with CPB = 0, K / 1024 of them read
 // at run time (K past 4096).
 //
@@ -197,13 +198,18 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 constexpr int kStreamEpFast = 0;
 constexpr int kStreamEpGeneric = 1;
 
-template <int CPB, int EPF>
+template <int CPB, int EPF, int MF>
 __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   constexpr int NW = 8;
   constexpr int CH = 16 * 2048;  // a chunk: 16 rows x 2 KB
   constexpr int NR = 4;          // ring slots
-  constexpr int RED = NR * CH;   // then the partial sums: [block parity][wave][lane], 16 B each
-  constexpr int EPV = RED + 2 * NW * 64 * 16;  // then the epilogue's vectors: [block % 3][cs, rs, ra][64 slots]
+  // then the partial sums: [block parity][wave][fragment][lane], 16 B each -- two parities
+  // with one 16-token fragment, one with two (a block's partial sums are read at the next
+  // block's first chunk and rewritten at its end, a barrier later: two fragments take only
+  // K of 2048 and up)
+  constexpr int NPAR = MF == 1 ? 2 : 1;
+  constexpr int RED = NR * CH;
+  constexpr int EPV = RED + NPAR * NW * MF * 64 * 16;  // then the epilogue's vectors: [block % 3][cs, rs, ra][64 slots]
   __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * 3 * 256];
 
   const int tid = threadIdx.x;
@@ -294,7 +300,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     };
     const int n = bi * 16 + l;
     if (cs_vec)
-      load(e.cs, (int64_t)(p.M - 1) * e.cs.ld + 1, l < 16 && l < p.M, (int64_t)l * e.cs.ld, base);
+      load(e.cs, (int64_t)(p.M - 1) * e.cs.ld + 1, l < 16 * MF && l < p.M, (int64_t)l * e.cs.ld, base);
     if (rs_vec) load(e.rs, p.N, l < 16 && n < p.N, n, base + 256);
     if (ra_vec) load(e.ra, p.N, l < 16 && n < p.N, n, base + 512);
   };
@@ -311,9 +317,14 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     return f32x4{word_val(s[0], o.dt, hi_half(o, n)), word_val(s[1], o.dt, hi_half(o, n + 1)),
                  word_val(s[2], o.dt, hi_half(o, n + 2)), word_val(s[3], o.dt, hi_half(o, n + 3))};
   };
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[MF];
+#pragma unroll
+  for (int f = 0; f < MF; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto red_at = [&](int j, int w2, int f) {  // a lane's 16 bytes of the partial sums
+    return (uint32_t)(RED + ((((MF == 1 ? j & 1 : 0) * NW + w2) * MF + f) * 64 + lane) * 16);
+  };
   // the MFMAs of this wave's group of chunk q (its slot landed and visible)
-  auto mma = [&](int q, const i32x4 (&xc)[4]) {
+  auto mma = [&](int q, const i32x4 (&xc)[MF][4]) {
     const uint32_t slot = (uint32_t)(q & (NR - 1)) * CH;
     i32x4 w[4];
 #pragma unroll
@@ -323,19 +334,23 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[s]),
-                                                    __builtin_bit_cast(bf16x8, xc[s]), acc, 0, 0, 0);
+#pragma unroll
+      for (int f = 0; f < MF; ++f)
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[s]),
+                                                         __builtin_bit_cast(bf16x8, xc[f][s]), acc[f], 0, 0, 0);
   };
-  // block j of this workgroup: its partial sums are at parity j & 1
+  // block j of this workgroup (its partial sums at parity j & 1 with one fragment)
   auto finish = [&](int j) {
     const int bi = block_of(j);
+#pragma unroll 1
+    for (int f = 0; f < MF; ++f) {
     i32x4 part[NW];
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) part[w2] = ds_read16(RED + (((j & 1) * NW + w2) * 64 + lane) * 16);
+    for (int w2 = 0; w2 < NW; ++w2) part[w2] = ds_read16(red_at(j, w2, f));
     f32x4 sum = __builtin_bit_cast(f32x4, part[0]);
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) sum += __builtin_bit_cast(f32x4, part[w2]);
-    const int m = rf, n = bi * 16 + 4 * kq;
+    const int m = 16 * f + rf, n = bi * 16 + 4 * kq;
     if (EPF == kStreamEpFast && fused) {
       const uint8_t* eo = ring + EPV + (j % 3) * 768;
       const f32x4 ra = ra_vec ? unpack_bf16x4(*(const u32x2*)(eo + 512 + 8 * kq))
@@ -353,6 +368,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       sum = act4(e.act, sum * (rs * cs) + ra + e.cadd);
     }
     if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
+    }
   };
 
   // X for chunk k (its group of this wave) goes to registers by loads issued just before
@@ -367,19 +383,23 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // wave 0's epilogue-vector DMAs of the step before (ep_load) are among them too
   const int nvec = EPF == kStreamEpFast ? (int)ra_vec : (int)cs_vec + (int)rs_vec + (int)ra_vec;
   auto wait_chunk = [&](int q, bool ep_before) {
-    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq) + has_x(q + 1)) + (ep_before && wave == 0 ? nvec : 0);
+    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq)) + 4 * MF * has_x(q + 1) + (ep_before && wave == 0 ? nvec : 0);
     switch (n) {
 #define HKX_WAIT_CASE(N) case N: __builtin_amdgcn_s_waitcnt(wait_vm_dec(N) & ~(15 << 8)); break;
       HKX_WAIT_CASE(1) HKX_WAIT_CASE(2) HKX_WAIT_CASE(3) HKX_WAIT_CASE(4) HKX_WAIT_CASE(5)
       HKX_WAIT_CASE(6) HKX_WAIT_CASE(7) HKX_WAIT_CASE(8) HKX_WAIT_CASE(9) HKX_WAIT_CASE(10)
       HKX_WAIT_CASE(11) HKX_WAIT_CASE(12) HKX_WAIT_CASE(13) HKX_WAIT_CASE(14) HKX_WAIT_CASE(15)
+      HKX_WAIT_CASE(16) HKX_WAIT_CASE(17) HKX_WAIT_CASE(18) HKX_WAIT_CASE(19)
 #undef HKX_WAIT_CASE
       default: __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8)); break;
     }
   };
   auto block_done = [&](int j) {
-    ds_write16(RED + (((j & 1) * NW + wave) * 64 + lane) * 16, __builtin_bit_cast(i32x4, acc));
-    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+      ds_write16(red_at(j, wave, f), __builtin_bit_cast(i32x4, acc[f]));
+      acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   };
   // This wave's share of X for chunk c (K group 8 c + wave: 16 rows x 256 bytes) in four
   // loads of whole 128-byte lines: load i brings rows 8 (i & 1) + [0, 8), line i >> 1 of
@@ -387,11 +407,15 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // line). In the MFMA layout -- lane l holding row l % 16 -- a load asks for 64 bytes of
   // 16 lines: measured 0.4-0.5 us slower at M = 16 (lines with the row in the low lane
   // bits were no faster either).
-  auto xload = [&](int c, i32x4 (&dst)[4]) {
+  // (with two 16-token fragments, fragment f the rows 16 f + [0, 16))
+  auto xload = [&](int c, i32x4 (&dst)[MF][4]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dst[i] = buf_load16(rx, (uint32_t)((lane >> 3) + 8 * (i & 1)) * p.lda_b + (uint32_t)(lane & 7) * 16 + (i >> 1) * 128,
-                          (uint32_t)(8 * kchunk(c) + wave) * 256u);
+    for (int f = 0; f < MF; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dst[f][i] = buf_load16(rx, (uint32_t)(16 * f + (lane >> 3) + 8 * (i & 1)) * p.lda_b + (uint32_t)(lane & 7) * 16 +
+                                       (i >> 1) * 128,
+                               (uint32_t)(8 * kchunk(c) + wave) * 256u);
   };
   // ... then into the MFMA layout, just before the chunk's MFMAs: k-step s = 2 h + e of lane
   // (rf, kq) takes row rf, piece 4 s + kq of the group, which load 2 h + rf / 8 holds at
@@ -402,7 +426,10 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // shuffle moved off the path to the MFMAs, measured slower.)
   const int xsrc0 = 4 * (8 * (rf & 7) + kq + 4 * (rf >> 3)), xsrc1 = 4 * (8 * (rf & 7) + kq + 4 * (rf < 8));
   const bool hi4 = (lane & 4) != 0;
-  auto xperm = [&](i32x4 (&v)[4]) {
+  auto xperm = [&](i32x4 (&vv)[MF][4]) {
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+    i32x4 (&v)[4] = vv[f];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -414,12 +441,13 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
         v[2 * h][d] = __builtin_amdgcn_ds_bpermute(xsrc0, m0);
         v[2 * h + 1][d] = __builtin_amdgcn_ds_bpermute(xsrc1, m1);
       }
+    }
   };
 
   if constexpr (CPB > 0) {
     // X held in registers for the whole walk, its chunks loaded with the first block's
     // fills, so a workgroup starts on 32 KB of X rather than all of it
-    i32x4 x[CPB][4];
+    i32x4 x[CPB][MF][4];
     ep_load(0);
     xload(0, x[0]);
     __builtin_amdgcn_sched_barrier(0);
@@ -448,8 +476,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   } else {
     // K past 4096: X streamed with the chunks through three register slots (the loop is
     // unrolled by three so every slot is a fixed register set)
-    i32x4 xs[3][4];
-    auto xnext = [&](int q, i32x4 (&dst)[4]) {
+    i32x4 xs[3][MF][4];
+    auto xnext = [&](int q, i32x4 (&dst)[MF][4]) {
       if (has_x(q)) xload(q % cpb, dst);
     };
     ep_load(0);
@@ -458,7 +486,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     xnext(1, xs[1]);
     fill(1);
     fill(2);
-    auto step = [&](int q, i32x4 (&xc)[4], i32x4 (&xn)[4]) {
+    auto step = [&](int q, i32x4 (&xc)[MF][4], i32x4 (&xn)[MF][4]) {
       const int j = q / cpb, c = q - j * cpb;
       wait_chunk(q, c == 1 && j + 1 < my_blocks);
       __builtin_amdgcn_s_barrier();

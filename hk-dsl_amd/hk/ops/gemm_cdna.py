@@ -157,9 +157,10 @@ def resolve(rec: Dict[str, Any], m: int, n: int, k: int, fp8: bool = False) -> D
     """A candidate made concrete for a shape: the decode kernel's split over K (enough
     workgroups for twice the CUs, at least four 128-element groups a split)."""
     rec = dict(rec)
-    if rec["kernel"] == "decode" and rec.get("variant", 0) & 1 and m <= 16 and k % 1024 == 0 \
-            and k <= 32768 and rec.get("splits") == "auto":
-        # the streaming kernel: one workgroup a CU walks all of W, no split
+    if rec["kernel"] == "decode" and rec.get("variant", 0) & 1 and k % 1024 == 0 and k <= 32768 \
+            and (m <= 16 or (m <= 32 and k >= 2048)) and rec.get("splits") == "auto":
+        # the streaming kernel: one workgroup a CU walks all of W, no split (two 16-token
+        # fragments from M = 17, with K of 2048 and up)
         rec["splits"] = 1
     if rec["kernel"] == "decode" and rec.get("splits") == "auto":
         wgs = math.ceil(n / (16 * (rec.get("rows", 16) // 16)))

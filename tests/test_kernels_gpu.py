@@ -327,13 +327,15 @@ def test_ring_falls_back_for_ragged_n():
     O.assert_close(c, O.gemm_fp32(a, b), rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 24, 32])
 @pytest.mark.parametrize("nk", [(1536, 4096), (1000, 2048), (12288, 1024), (256, 1024), (4100, 3072),
                                 (4096, 12288), (1000, 14336), (300, 5120), (16, 6144)])
 def test_decode_stream(m, nk):
-    """The streaming decode kernel (M <= 16, K a multiple of 1024; past 4096 X is streamed
-    with the chunks): bias epilogue, ragged N (rows of W past N read as zeros, columns
-    past N never written), chunk counts per workgroup from 1 up (3 ahead of the ring)."""
+    """The streaming decode kernel (M <= 16, or M <= 32 as two 16-token fragments from K =
+    2048; K a multiple of 1024; past 4096 X is streamed with the chunks): bias epilogue,
+    ragged N (rows of W past N read as zeros, columns past N never written), ragged M
+    (rows past M never written), chunk counts per workgroup from 1 up (3 ahead of the
+    ring). At K = 1024 and M > 16 the call goes to decode_kernel."""
     n, k = nk
     a, b = _data(m, n, k, seed=25)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(26)).to(torch.bfloat16)
@@ -346,7 +348,7 @@ def test_decode_stream(m, nk):
     assert (c[:, n:].float() == 7.0).all()
 
 
-@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("m", [1, 7, 16, 20, 32])
 @pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024), (1000, 6144)])
 def test_decode_stream_fused_forms(m, nk):
     """The streaming decode kernel's whole fused form: a per-token scale with a stride (a
