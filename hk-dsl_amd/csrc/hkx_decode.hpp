@@ -407,15 +407,22 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // line). In the MFMA layout -- lane l holding row l % 16 -- a load asks for 64 bytes of
   // 16 lines: measured 0.4-0.5 us slower at M = 16 (lines with the row in the low lane
   // bits were no faster either).
-  // (with two 16-token fragments, fragment f the rows 16 f + [0, 16))
+  // (with two 16-token fragments, fragment f the rows 16 f + [0, 16)). Up to M = 8 the loads
+  // are in the MFMA layout instead (lane l: row l % 16, 16 bytes at 16 (l / 16) + 64 i):
+  // there X is a few KB a CU, rows past M read nothing, and the shuffle below would only
+  // add its latency to every chunk of the first block (1-2 us at M = 1 on the shapes whose
+  // workgroups have one block).
+  const bool xlines = MF == 2 || p.M > 8;
   auto xload = [&](int c, i32x4 (&dst)[MF][4]) {
 #pragma unroll
     for (int f = 0; f < MF; ++f)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dst[f][i] = buf_load16(rx, (uint32_t)(16 * f + (lane >> 3) + 8 * (i & 1)) * p.lda_b + (uint32_t)(lane & 7) * 16 +
-                                       (i >> 1) * 128,
-                               (uint32_t)(8 * kchunk(c) + wave) * 256u);
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t off = xlines ? (uint32_t)(16 * f + (lane >> 3) + 8 * (i & 1)) * p.lda_b +
+                                          (uint32_t)(lane & 7) * 16 + (i >> 1) * 128
+                                    : (uint32_t)rf * p.lda_b + kq * 16 + i * 64;
+        dst[f][i] = buf_load16(rx, off, (uint32_t)(8 * kchunk(c) + wave) * 256u);
+      }
   };
   // ... then into the MFMA layout, just before the chunk's MFMAs: k-step s = 2 h + e of lane
   // (rf, kq) takes row rf, piece 4 s + kq of the group, which load 2 h + rf / 8 holds at
@@ -427,6 +434,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const int xsrc0 = 4 * (8 * (rf & 7) + kq + 4 * (rf >> 3)), xsrc1 = 4 * (8 * (rf & 7) + kq + 4 * (rf < 8));
   const bool hi4 = (lane & 4) != 0;
   auto xperm = [&](i32x4 (&vv)[MF][4]) {
+    if (!xlines) return;
 #pragma unroll
     for (int f = 0; f < MF; ++f) {
     i32x4 (&v)[4] = vv[f];
