@@ -164,8 +164,6 @@ def stream_of(device) -> int:
 
 
 _WS: dict = {}
-#: Every workspace a captured CUDA graph has used: kept until the process ends.
-_PINNED: list = []
 
 
 def capturing(device) -> bool:
@@ -180,22 +178,22 @@ def workspace(device, nbytes: int):
     reference's module-owned scratch (python/hk/ops/gemm_cdna_dp.py:330-338). Calls on
     one stream run in order, so they can share it.
 
-    Under CUDA-graph capture a graph bakes the buffer's address in, so each captured call
-    gets a buffer of its own that is never freed (kept for the life of the process): a
-    shared one could be freed when a bigger one replaced it in the cache -- and
-    torch.cuda.graph's empty_cache() before the next capture would unmap it under a graph
-    that still replays it -- and two graphs replayed at once on different streams would
-    race on it."""
+    Under CUDA-graph capture a graph bakes the buffer's address in, so a captured call gets
+    a buffer of its own, allocated in the capture -- i.e. from the graph's private memory
+    pool, which lives exactly as long as the graph -- and not kept here: the caller holds it
+    until its launches are enqueued, after which the capture may hand the same memory to a
+    later allocation of the same graph (that runs after those launches on the stream, as
+    any temporary of a captured region). The eager cache is never used in a capture: its
+    buffer could be replaced (and freed) under a graph still replaying it, and two graphs
+    replayed at once on different streams would share it. (Keeping every captured call's
+    buffer for the life of the process, as an earlier form did, grows without bound in a
+    process that captures many graphs.)"""
     import torch  # noqa: PLC0415
 
     if nbytes == 0:
         return None
     if capturing(device):
-        # a buffer of this capture's own, kept for the life of the process: two graphs
-        # replayed at once on different streams must not share one
-        buf = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
-        _PINNED.append(buf)
-        return buf
+        return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
     key = (device, stream_of(device))
     buf = _WS.get(key)
     if buf is None or buf.numel() * 4 < nbytes:

@@ -109,3 +109,45 @@ def test_scaled_mm_with_number_scales_replays(scalar_first):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}"
+
+
+def test_captured_workspaces_go_with_their_graphs():
+    """A split-K call captured into a graph allocates its workspace in the capture, so the
+    memory belongs to the graph and goes with it: capturing and dropping graphs over and
+    over (a tuner, or an engine re-capturing its batch sizes) holds no memory per captured
+    call, and every replay before the drop is still right."""
+    m, n, k = 16, 4096, 4096
+    gen = torch.Generator().manual_seed(42)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, k, generator=gen) * k ** -0.5).to(torch.bfloat16).to(DEV)
+    ref = T(x, w, schedule="t64k8").clone()
+    out = torch.empty_like(ref)
+
+    side = torch.cuda.Stream()   # one warm-up stream: its eager workspace is cached once
+
+    def once():
+        fn = lambda: T(x, w, out=out, schedule="t64k8")  # noqa: E731
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        out.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        del g
+
+    for _ in range(3):
+        once()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    for i in range(30):
+        print(f"capture {i}", flush=True)
+        once()
+    torch.cuda.synchronize()
+    ws = 8 * m * n * 4    # one captured call's workspace: 8 fp32 shares of (M, N)
+    assert torch.cuda.memory_allocated() - base < 2 * ws
