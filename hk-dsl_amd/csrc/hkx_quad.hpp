@@ -299,43 +299,62 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
           for (int f = 0; f < 2; ++f) cs[i][f] = ((const float*)ev)[128 * i + 64 * grp + 32 * f + rf];
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int cb = 128 * j + 32 * wc;  // the block's first column
+        [[maybe_unused]] f32x4 rs[2][2], bv[2][2];  // [run t][u]
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          __builtin_amdgcn_sched_barrier(0);
-          const int c0 = 128 * j + 32 * wc + 16 * t;
-          [[maybe_unused]] f32x4 rs[2], bv[2];
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int col = c0 + 8 * u + 4 * h;
-            if constexpr (deq) rs[u] = *(const f32x4*)(ev + 1024 + col * 4);
-            if constexpr (bias) bv[u] = unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
+            const int col = cb + 16 * t + 8 * u + 4 * h;
+            if constexpr (deq) rs[t][u] = *(const f32x4*)(ev + 1024 + col * 4);
+            if constexpr (bias) bv[t][u] = unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
           }
+        // after the 16-lane trade below, lane l stores row 16 s + l % 16 of the fragment
+        // (s: which of the two registers), columns 16 ((l >> 4) & 1) + 8 (l >> 5) + [0, 8)
+        // of the block: each store covers 16 rows x 64 contiguous bytes (four lanes a row),
+        // not 32 rows x 32 bytes (a 33 MB burst of C measured 2.9 TB/s in 32-byte pieces,
+        // 3.3 in 64-byte ones)
+        const int n = cb + 16 * ((lane >> 4) & 1) + 8 * (lane >> 5);
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int f = 0; f < 2; ++f) {
-              const int ml = 128 * i + 64 * grp + 32 * f + rf;
+          for (int f = 0; f < 2; ++f) {
+            uint32_t T[2][4];  // [run t]: lane (rf, h)'s columns 16 t + 8 h + [0, 8) of row rf
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
               f32x4 v[2];
 #pragma unroll
               for (int u = 0; u < 2; ++u) {
                 const Acc& a = acc[i][j][f][0];
                 const int r = 8 * t + 4 * u;
                 v[u] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
-                if constexpr (deq) v[u] = v[u] * (rs[u] * cs[i][f]);
-                if constexpr (bias) v[u] += bv[u];
+                if constexpr (deq) v[u] = v[u] * (rs[t][u] * cs[i][f]);
+                if constexpr (bias) v[u] += bv[t][u];
               }
               const u32x2 w0 = pack4<2>(HKX_BF16, v[0]), w1 = pack4<2>(HKX_BF16, v[1]);
               uint32_t x0 = w0.x, x1 = w1.x, y0 = w0.y, y1 = w1.y;
               swap32(x0, x1);
               swap32(y0, y1);
-              const int n = c0 + 8 * h;
+              T[t][0] = x0;
+              T[t][1] = y0;
+              T[t][2] = x1;
+              T[t][3] = y1;
+            }
+            // rows 0-15 of both runs into T[0], rows 16-31 into T[1]
+#pragma unroll
+            for (int d = 0; d < 4; ++d) swap16(T[0][d], T[1][d]);
+#pragma unroll
+            for (int sr = 0; sr < 2; ++sr) {
+              const int ml = 128 * i + 64 * grp + 32 * f + 16 * sr + (lane & 15);
               if (n0 + n < p.N)
                 __builtin_amdgcn_raw_buffer_store_b128(
-                    i32x4{(int)x0, (int)y0, (int)x1, (int)y1}, rc,
+                    i32x4{(int)T[sr][0], (int)T[sr][1], (int)T[sr][2], (int)T[sr][3]}, rc,
                     (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u, 0, 0);
             }
-        }
+          }
+      }
     } else {
     const int rf = lane & 15, q = lane >> 4;
     [[maybe_unused]] f32x4 bv[2][2];
