@@ -164,10 +164,9 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 
 
 // The streaming decode GEMM: one workgroup a CU walks its share of the 16-row blocks of W
-// (a consecutive run of them), for M <= 32 (MF = 1 or 2 16-token fragments; two from K = 2048
-// up), unpaired, no split, K a multiple of
-// 1024: CPB chunks of 1024 a block (CPB = 1..4), or, with CPB = 0, K / 1024 of them read
-// at run time (K past 4096).
+// (a consecutive run of them), for M <= 32 (MF = 1 or 2 16-token fragments; two from
+// K = 2048 up), unpaired, no split, K a multiple of 1024: CPB chunks of 1024 a block
+// (CPB = 1..4), or, with CPB = 0, K / 1024 of them read at run time (K past 4096).
 //
 // * W goes HBM -> LDS by non-temporal buffer loads (`buffer_load_dwordx4 ... lds`, read
 //   once, kept out of the caches), each instruction 1 KB
@@ -177,16 +176,18 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
 //   row (piece c at c ^ (r % 16)), applied on the global side, so the MFMA fragment reads
 //   (16 rows, one piece each) are conflict-free.
 // * X is the same for every block: wave w owns the 128-element group w of every chunk, and
-//   loads its share of X (CPB groups of 16 rows) into registers once, a chunk's share with
-//   the first block's fill of the chunk before it (all of X up front cost 1 us of
+//   loads its share of X (CPB groups of 16 or 32 rows) into registers once, a chunk's share
+//   with the first block's fill of the chunk before it (all of X up front cost 1 us of
 //   20 at M = 16, K = 4096); past K = 4096 it is streamed with the chunks instead (two
-//   chunks ahead, three register slots).
+//   chunks ahead, three register slots). Above M = 8 it arrives as whole 128-byte lines
+//   and is shuffled into the MFMA layout before the chunk's MFMAs (see xload / xperm).
 //   Each step issues its X loads before its fill, so the waits, which count loads in issue
 //   order, wait for exactly the chunk and the X they need (the compiler's own order put X
 //   after the fill, which made the register waits take the next chunk's fill too: 0.4 us
 //   at M = 16).
 // * v_mfma_f32_16x16x32_bf16 with W's fragment first; the 8 waves' partial sums of a block
-//   meet in LDS (double-buffered by block parity), and wave 0 sums, applies the epilogue and
+//   meet in LDS (double-buffered by block parity with one fragment, one buffer with two),
+//   and wave 0 sums, applies the epilogue and
 //   stores after the next chunk's barrier, under the other waves' MFMAs. The epilogue's
 //   common form (a bf16 bias, an activation) reads its bias with one LDS read a lane; a
 //   wait it had on a tile operand's direct load, and element-by-element vector reads,
