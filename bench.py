@@ -10,7 +10,10 @@ resident in HBM before the timed region.
 
 Prints ONE JSON line: the metric and its value (whole-job TFLOP/s), the roofline of the
 dominant kernel (achieved TFLOP/s from HIP events around each launch, against the
-2.5 PFLOP/s bf16 dense peak), the CPU baseline (the oracle, torch fp32 on the host
+2.5 PFLOP/s bf16 dense peak, and against this GPU's own ceilings measured in the same run:
+a register-only MFMA loop on constant operands, and the same loop on random operands --
+the rate the board's power limit allows on data that toggles like real tensors), the CPU
+baseline (the oracle, torch fp32 on the host
 cores, on a bounded sample), and, under "also", the other BASELINE configs measured the
 same way: the fused gate_up + silu_and_mul GEMM, the decode GEMMs (HBM GB/s of W, with
 weight copies rotated past the 256 MB Infinity Cache; kernel time from a replayed graph,
