@@ -122,7 +122,8 @@ def _hk_takes(path: str, m: int, n: int, k: int) -> bool:
     from ..ops import gemm_cdna  # noqa: PLC0415
 
     if path == "hk":
-        return n % gemm_cdna.BLOCK_N_MIN == 0 and k % gemm_cdna.K_STEP == 0
+        return (n % gemm_cdna.BLOCK_N_MIN == 0 and k % gemm_cdna.K_STEP == 0
+                and 2 * max(m, n) * k < gemm_cdna.OPERAND_BYTES_MAX)
     if path == "hk_decode":
         return gemm_cdna.fits("decode", m, n, k)
     return False

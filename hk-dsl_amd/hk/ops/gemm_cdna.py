@@ -26,6 +26,9 @@ from typing import Any, Dict, Optional
 #: Multiples the kernels need: K in 128-byte stages (64 bf16), N in 4s.
 K_STEP = 64
 BLOCK_N_MIN = 4
+#: A and B are read through buffer resources with 32-bit byte offsets: each spans less
+#: than 4 GiB (hkx_gemm refuses larger ones).
+OPERAND_BYTES_MAX = 1 << 32
 #: CUs of an MI355X.
 CUS = 256
 
@@ -103,7 +106,7 @@ def fits(name: str, m: int, n: int, k: int, fp8: bool = False) -> bool:
     if c is None or m < 1 or n % BLOCK_N_MIN:
         return False
     kstep = 128 if fp8 else 64
-    if k % kstep:
+    if k % kstep or max(m, n) * k * (1 if fp8 else 2) >= OPERAND_BYTES_MAX:
         return False
     if c["kernel"] == "decode":
         return not fp8 and m <= 32 and k % 128 == 0
@@ -183,4 +186,4 @@ def matmul(a, b, out=None):
 
 __all__ = ["CANDIDATES", "OVERRIDE", "route", "rule", "resolve", "fits", "matmul", "table",
            "reload_table",
-           "K_STEP", "BLOCK_N_MIN", "CUS"]
+           "K_STEP", "BLOCK_N_MIN", "OPERAND_BYTES_MAX", "CUS"]

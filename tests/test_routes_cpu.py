@@ -125,3 +125,34 @@ def test_shipped_mxfp8_table_is_its_own_decision():
                     assert want == "hk"
     finally:
         V.set_routes(None)
+
+
+def test_operands_of_4_gib_take_no_kernel(monkeypatch):
+    # hkx_gemm refuses an A or B of 4 GiB or more (32-bit buffer offsets), so neither the
+    # template's candidates nor the engine route may send one there: a bf16 weight of
+    # 131072 x 16384 (exactly 4 GiB) or 131072 tokens of K = 16384 go to the engine's own
+    # GEMM; one row fewer is taken
+    from hk.integration import vllm_gemm
+
+    assert gemm_cdna.OPERAND_BYTES_MAX == 1 << 32
+    assert gemm_cdna.fits("decode", 8, 131068, 16384)
+    assert not gemm_cdna.fits("decode", 8, 131072, 16384)
+    assert gemm_cdna.fits("t256", 4096, 131068, 16384)
+    assert not gemm_cdna.fits("t256", 131072, 4096, 16384)
+    assert not gemm_cdna.fits("t256", 4096, 131072, 16384)
+    assert gemm_cdna.fits("t256", 4096, 131072, 16384, fp8=True)
+
+    class Everywhere:
+        def __init__(self, path):
+            self.path = path
+
+        def lookup(self, m, n, k):
+            return self.path
+
+    for path in ("hk", "hk_decode"):
+        monkeypatch.setattr(vllm_gemm, "routes", lambda p=path: Everywhere(p))
+        assert vllm_gemm.route_for(8, 131068, 16384) == path
+        assert vllm_gemm.route_for(8, 131072, 16384) == "fallback"
+    monkeypatch.setattr(vllm_gemm, "routes", lambda: Everywhere("hk"))
+    assert vllm_gemm.route_for(131072, 4096, 16384) == "fallback"
+    assert vllm_gemm.route_for(131071, 4096, 16384) == "hk"
