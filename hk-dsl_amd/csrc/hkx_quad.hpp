@@ -19,8 +19,9 @@
 // * Phases. Per K-tile t, two phases, each: LDS reads into registers, fills, a barrier,
 //   the MFMAs of two blocks (32 v_mfma_f32_16x16x32_bf16, or 8 fp8 32 x 32 x 64), a
 //   barrier:
-//     1: read A0(t), B0(t), B1(t); fill A1(t + 1);                 math (0, 0), (0, 1)
-//     2: read A1(t);               fill B0, B1, A0 of t + 2;       math (1, 0), (1, 1)
+//     1: read A0(t), B0(t);      fill A1(t + 1), B1(t + 2);   math (0, 0), (0, 1)
+//     2: read A1(t), B1(t + 1);  fill B0, A0 of t + 2;         math (1, 0), (1, 1)
+//   (the MX form reads B1(t) in phase 1 and fills B1(t + 2) in phase 2 with B0 and A0).
 //   A quarter is refilled only in a phase after both groups read it (group 1 runs one
 //   barrier behind group 0, so its reads of phase k land under group 0's MFMAs of phase
 //   k); each fill is about three phases ahead of its first read. Before each barrier a
@@ -207,7 +208,8 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   }
   constexpr int NA = FP8 ? 2 : 4, NB = FP8 ? 1 : 2;  // fragments of a block's A and B rows
   using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
-  Frag af[NA][2], bf0[NB][2], bf1[NB][2];  // [fragment][K-half]
+  // [fragment][K-half]; bfn: B1 of the next K-tile (see the K loop)
+  Frag af[NA][2], bf0[NB][2], bf1[NB][2], bfn[NB][2];
   auto frag_at = [&](const uint8_t* s, int r0, int h, int par) -> Frag {
     if constexpr (FP8) {
       const i32x4 lo = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[0]);
@@ -441,51 +443,85 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
+  // Without MX, phase 2 also reads B1 of the next K-tile (into the other of bf1 / bfn, the
+  // two alternating by K-tile) and B1's fill moves to phase 1, two K-tiles ahead: each phase
+  // then reads 12 fragments and issues 4 fills, where phase 1 read 16 and issued 2 (config 2
+  // 1-3% faster). Every quarter is still refilled only after both groups read it and about
+  // three phases before its first read, and the fills keep the order of their reads, so the
+  // waits stay "all but the newest 8". The MX form keeps B1 in phase 1: its scales leave
+  // no registers for the second B1 set.
+  constexpr bool B1N = !MX;
   vec_load(0);
   Stream s1 = stream_at(0), s2 = stream_at(0);
-  fill(2, s2);
-  scale_fill(s2);
-  fill(3, s2);
-  fill(0, s2);
-  fill(1, s1);
-  advance(s1);
-  advance(s2);
-  fill(2, s2);
-  scale_fill(s2);
-  fill(3, s2);
-  fill(0, s2);
-  advance(s2);
-  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // A0, B0 and B1 of K-tile 0
-  __builtin_amdgcn_s_barrier();
-  if (grp == 1) __builtin_amdgcn_s_barrier();
-  int g = 0;
-  for (int lt = 0; lt < my_tiles; ++lt) {
-    for (int t = 0; t < nkt; ++t, ++g) {
-      const int slot = g & 1;
-      const bool z = t == 0;
-      // phase 1
-      read_a(slot, 0);
-      read_b(slot, 0, bf0);
-      read_b(slot, 1, bf1);
-      read_scales(lt, t);
-      if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {  // K-tile 0 whole, then K-tile 1 but A1, in steady-state order
+    if constexpr (B1N) fill(3, s2);
+    fill(2, s2);
+    scale_fill(s2);
+    if constexpr (!B1N) fill(3, s2);
+    fill(0, s2);
+    if (r == 0) {
       fill(1, s1);
       advance(s1);
-      sync_mem();
-      math(0, 0, bf0, z);
-      math(0, 1, bf1, z);
-      sync_math();
-      // phase 2
-      read_a(slot, 1);
-      fill(2, s2);
-      scale_fill(s2);
-      fill(3, s2);
-      fill(0, s2);
-      advance(s2);
-      sync_mem();
-      math(1, 0, bf0, z);
-      math(1, 1, bf1, z);
-      sync_math();
+    }
+    advance(s2);
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // A0, B0 and B1 of K-tile 0
+  __builtin_amdgcn_s_barrier();
+  if constexpr (B1N) {  // B1 of K-tile 0, read by every wave before any refill of it
+    read_b(0, 1, bf1);
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
+    __builtin_amdgcn_s_barrier();
+  }
+  if (grp == 1) __builtin_amdgcn_s_barrier();
+  // K-tile t of local tile lt, the workgroup's g-th: b1 holds its B1 fragments, nb1 takes
+  // the next K-tile's (B1N)
+  auto ktile = [&](int lt, int t, int g, Frag (&b1)[NB][2], Frag (&nb1)[NB][2]) {
+    const int slot = g & 1;
+    const bool z = t == 0;
+    // phase 1
+    read_a(slot, 0);
+    read_b(slot, 0, bf0);
+    if constexpr (!B1N) read_b(slot, 1, b1);
+    read_scales(lt, t);
+    if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
+    fill(1, s1);
+    advance(s1);
+    if constexpr (B1N) fill(3, s2);
+    sync_mem();
+    math(0, 0, bf0, z);
+    math(0, 1, b1, z);
+    sync_math();
+    // phase 2
+    read_a(slot, 1);
+    if constexpr (B1N) read_b(slot ^ 1, 1, nb1);
+    fill(2, s2);
+    scale_fill(s2);
+    if constexpr (!B1N) fill(3, s2);
+    fill(0, s2);
+    advance(s2);
+    sync_mem();
+    math(1, 0, bf0, z);
+    math(1, 1, b1, z);
+    sync_math();
+  };
+  int g = 0;
+  for (int lt = 0; lt < my_tiles; ++lt) {
+    if constexpr (B1N) {
+      int t = 0;
+      for (; t + 1 < nkt; t += 2, g += 2) {
+        ktile(lt, t, g, bf1, bfn);
+        ktile(lt, t + 1, g + 1, bfn, bf1);
+      }
+      if (t < nkt) {  // an odd count: the last K-tile, and the next tile's B1 back in bf1
+        ktile(lt, t, g++, bf1, bfn);
+#pragma unroll
+        for (int f = 0; f < NB; ++f)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) bf1[f][h] = bfn[f][h];
+      }
+    } else {
+      for (int t = 0; t < nkt; ++t, ++g) ktile(lt, t, g, bf1, bf1);
     }
     epilogue(lt);
   }
