@@ -73,7 +73,7 @@ int wave_cut(int m, int n, int outw);
 
 bool tile_shape_ok(int bm, int bn) {
   return (bm == 256 && bn == 256) || (bm == 128 && bn == 256) || (bm == 64 && bn == 256) ||
-         (bm == 128 && bn == 128) || (bm == 256 && bn == 128);
+         (bm == 128 && bn == 128) || (bm == 256 && bn == 128) || (bm == 64 && bn == 128);
 }
 
 int wave_rows(int bm, int bn) {  // waves along M for a tile shape
@@ -229,11 +229,14 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   p->pair = pair;
   if (kernel == HKX_KERNEL_TILE) {
     if (!tile_shape_ok(bm, bn))
-      return fail(HKX_ERR_ARG, "tile %dx%d: 256x256, 128x256, 64x256, 128x128 or 256x128", bm, bn);
+      return fail(HKX_ERR_ARG, "tile %dx%d: 256x256, 128x256, 64x256, 128x128, 256x128 or 64x128",
+                  bm, bn);
     p->tile_m = bm;
     p->tile_n = bn;
     p->wm = wave_rows(bm, bn);
-    const bool four_ok = bn == 256 && (bm == 256 || bm == 128 || bm == 64);
+    const bool four_ok = (bn == 256 && (bm == 256 || bm == 128 || bm == 64)) ||
+                         (bn == 128 && (bm == 128 || bm == 64));
+    const bool eight_ok = !(bm == 64 && bn == 128);
     const bool pp_ok = bn == 256 && bm == 256;
     int sc = a->tile_schedule;
     if (sc == HKX_TILE_AUTO) sc = pp_ok ? HKX_TILE_RING : (four_ok ? HKX_TILE_W4 : HKX_TILE_W8);
@@ -242,7 +245,11 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     if (sc == HKX_TILE_RING && !pp_ok)
       return fail(HKX_ERR_ARG, "the ring tile kernel takes 256x256 tiles");
     if (sc == HKX_TILE_W4 && !four_ok)
-      return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256 or 64x256 tiles");
+      return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256, 64x256, 128x128 "
+                  "or 64x128 tiles");
+    if (sc == HKX_TILE_W8 && !eight_ok)
+      return fail(HKX_ERR_ARG, "the 8-wave tile kernel takes 256x256, 128x256, 64x256, 128x128 "
+                  "or 256x128 tiles");
     if (sc == HKX_TILE_PINGPONG && !pp_ok)
       return fail(HKX_ERR_ARG, "the ping-pong tile kernel takes 256x256 tiles");
     if (sc == HKX_TILE_RING ? (a->variant & ~(HKX_RING_WAVESPLIT | HKX_RING_STREAMK | HKX_RING_HALFSTAGE)) != 0 ||
@@ -395,6 +402,10 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
     return hkx::launch_pp(t, fp8, mode, !(p.variant & HKX_PP_MFMA32), g, s);
   }
   if (p.schedule == HKX_TILE_W4) {
+    if (bn == 128) {
+      if (bm == 128) return hkx::launch_tile4<128, 128>(t, fp8, mode, grid, s);
+      return hkx::launch_tile4<64, 128>(t, fp8, mode, grid, s);
+    }
     if (bm == 256) return hkx::launch_tile4<256, 256>(t, fp8, mode, grid, s);
     if (bm == 128) return hkx::launch_tile4<128, 256>(t, fp8, mode, grid, s);
     return hkx::launch_tile4<64, 256>(t, fp8, mode, grid, s);

@@ -10,8 +10,11 @@
 //   never touches a VGPR. Wave w's i-th load fills bytes [1024 w + 4096 i, +1024) of the
 //   stage; lane l's 16 bytes land at +16 l, so the XOR swizzle is chosen on the global
 //   side (lane l fetches logical chunk (l & 7) ^ swz(row & 15) of its row).
-// * Two LDS stages; the fill of stage kt + 2 is issued right after the one barrier of
-//   iteration kt and has a whole iteration to land.
+// * NST LDS stages, as many as fit up to four: four at BN = 128 (4 x 24 or 32 KB), three
+//   at 128 x 256 and 64 x 256 (3 x 48 or 40 KB), two at 256 x 256.
+//   The fills of tile kt + NST go into the stage iteration kt read, begun right after its
+//   one barrier and spread under the next iteration's k-steps; with three stages they have
+//   one iteration more to land (a wave a SIMD has nothing else to hide their latency with).
 // * Fragment reads are software-pipelined one k-step ahead (two register sets), and the
 //   reads of the next stage's first k-step are issued under the last k-step's MFMAs.
 // * MFMA: v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x64_f8f6f4 (fp8 e4m3), B's fragment
@@ -26,6 +29,9 @@
 namespace hkx {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+constexpr int tile4_vmcnt_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
 template <int BM, int BN, bool FP8, int MODE, int ACT = -1>
 __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
@@ -42,9 +48,13 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   constexpr bool STAGED = (MODE == kStore16 || MODE == kStore8 || MODE == kPair16);
   constexpr int RS = OUTW * OB + 16;  // staging row stride, bytes
   constexpr int STAGING = STAGED ? BM * RS : 0;
-  constexpr int ROWOP = (2 * STAGE > STAGING) ? 2 * STAGE : STAGING;  // + the row operands
+  // LDS stages: as many as fit beside the row operands, up to four
+  constexpr int NST = 4 * STAGE + 2 * BN * 4 <= 160 * 1024   ? 4
+                      : 3 * STAGE + 2 * BN * 4 <= 160 * 1024 ? 3
+                                                             : 2;
+  constexpr int ROWOP = (NST * STAGE > STAGING) ? NST * STAGE : STAGING;  // + the row operands
   constexpr int SMEM = ROWOP + 2 * BN * 4;
-  static_assert(FM >= 1 && FN >= 1 && BM % 64 == 0 && BN == 256, "tiling");
+  static_assert(FM >= 1 && FN >= 1 && BM % 64 == 0 && (BN == 256 || BN == 128), "tiling");
   static_assert(!PAIR || FN % 2 == 0, "the paired form needs gate/up fragment pairs");
   static_assert(SMEM <= 160 * 1024, "LDS");
   using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
@@ -183,11 +193,28 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
     csv[i] = (fused && e.cs.p && m < p.M) ? ld_col(e.cs, m) * e.cmul : e.cmul;
   }
 
-  // ---- prologue: stages 0 and 1 in flight, stage 0 landed, its first fragments read
-  fill_part(0, 0, 0, NCH);
-  if (nkt > 1) fill_part(1, 1, 0, NCH);
-  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): stages 0 and 1 landed
-  __syncthreads();
+  // ---- prologue: stages 0 .. NST - 2 in flight and the first fills of stage NST - 1 (as
+  // the barrier before iteration 0 would have issued them), stage 0 landed, its first
+  // fragments read. Every wait below is "all but this wave's newest n fill instructions"
+  // (buffer loads complete in order) followed by a bare s_barrier: __syncthreads()'s fence
+  // would wait for every fill in flight, the next stages' included.
+  constexpr int F0 = NCH * 3 / 8;  // fills of a stage issued at the barrier that frees it
+  // at iteration kt's barrier the newest fills are those of tiles kt + 2 .. kt + NST - 1
+  // (whole: the last one's began at the barrier before); in the prologue, those of stages
+  // 1 .. NST - 2 and the first F0 of stage NST - 1
+  constexpr int WAIT_LOOP = (NST - 2) * NCH;
+  constexpr int WAIT_PRO = (NST - 2) * NCH + F0;
+  auto sync_fills = [&](bool prologue) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (prologue) __builtin_amdgcn_s_waitcnt(tile4_vmcnt_lgkm0(WAIT_PRO));
+    else __builtin_amdgcn_s_waitcnt(tile4_vmcnt_lgkm0(WAIT_LOOP));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int st = 0; st < NST - 1; ++st) fill_part(min(st, nkt - 1), st, 0, NCH);
+  fill_part(min(NST - 1, nkt - 1), NST - 1, 0, F0);
+  sync_fills(true);
   read_frags(0, 0, a0, b0);
 
   // One iteration is one 128-byte K stage: KS k-steps of FM x FN MFMAs, fragment reads one
@@ -201,8 +228,9 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   // they still land before the barrier that waits for them.
   constexpr int NRD = FP8 ? 2 * (FM + FN) : (FM + FN);  // ds_read_b128 per k-step
   for (int kt = 0; kt < nkt; ++kt) {
-    const int s = kt & 1;
-    const int tk = min(kt + 1, nkt - 1);
+    const int s = kt % NST;
+    const int tk = min(kt + NST - 1, nkt - 1);  // the tile whose fills go on under this one
+    const int sf = (kt + NST - 1) % NST;        // and its stage
 #pragma unroll
     for (int ks = 0; ks < KS - 1; ++ks) {
       if (ks & 1) {
@@ -214,12 +242,12 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
       }
       {
         // the rest of tile kt + 1's fills, begun under iteration kt - 1's last k-step
-        constexpr int F0 = NCH * 3 / 8, F1 = NCH * 11 / 16;
+        constexpr int F1 = NCH * 11 / 16;
         if (KS == 2) {
-          fill_part(tk, s ^ 1, F0, NCH);
+          fill_part(tk, sf, F0, NCH);
         } else {
-          if (ks == 0) fill_part(tk, s ^ 1, F0, F1);
-          if (ks == 1) fill_part(tk, s ^ 1, F1, NCH);
+          if (ks == 0) fill_part(tk, sf, F0, F1);
+          if (ks == 1) fill_part(tk, sf, F1, NCH);
         }
 #pragma unroll
         for (int q = 0; q < NRD; ++q) {
@@ -233,14 +261,12 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     // every wave is done reading stage s once this barrier passes (its last reads were
-    // waited for), and stage s ^ 1 -- the next tile -- has landed: each wave waits for its
-    // own fills first (the barrier's fence waits only for LDS operations, not for these
-    // buffer loads)
-    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-    __syncthreads();
-    fill_part(min(kt + 2, nkt - 1), s, 0, NCH * 3 / 8);
+    // waited for), and the next stage -- tile kt + 1 -- has landed: each wave waits for its
+    // own fills of it: all but its newest (NST - 2) NCH
+    sync_fills(false);
+    fill_part(min(kt + NST, nkt - 1), s, 0, F0);
     // KS is even: step KS-1 multiplies set 1 while the next stage's step 0 reads set 0
-    read_frags(s ^ 1, 0, a0, b0);
+    read_frags((kt + 1) % NST, 0, a0, b0);
     mma(a1, b1);
 #pragma unroll
     for (int q = 0; q < NRD; ++q) {

@@ -63,6 +63,16 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},
     "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 4},
     "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 8},
+    # 128-column tiles on the 4-wave kernel (four LDS stages): twice the tiles of the
+    # 256-column ones at mid M, so fewer splits fill the CUs (gemm_cdna_dp.py's dp64 / dp128
+    # blocks are 128 columns wide)
+    "t128x128": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "schedule": "w4"},
+    "t128x128k2": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "schedule": "w4", "splits": 2},
+    "t128x128k4": {"kernel": "tile", "tile_m": 128, "tile_n": 128, "schedule": "w4", "splits": 4},
+    "t64x128": {"kernel": "tile", "tile_m": 64, "tile_n": 128, "schedule": "w4"},
+    "t64x128k2": {"kernel": "tile", "tile_m": 64, "tile_n": 128, "schedule": "w4", "splits": 2},
+    "t64x128k4": {"kernel": "tile", "tile_m": 64, "tile_n": 128, "schedule": "w4", "splits": 4},
+    "t64x128k8": {"kernel": "tile", "tile_m": 64, "tile_n": 128, "schedule": "w4", "splits": 8},
     "decode": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto", "variant": 1},
     "decode_blk": {"kernel": "decode", "waves": 8, "rows": 16, "splits": "auto"},
     "decode_w4": {"kernel": "decode", "waves": 4, "rows": 16, "splits": "auto"},

@@ -162,8 +162,10 @@ typedef struct HkxEpilogue {
 /* Tile kernel schedules (HkxGemmArgs.tile_schedule). */
 #define HKX_TILE_AUTO 0
 #define HKX_TILE_PINGPONG 1 /* 8 waves, two a SIMD taking turns at the MFMA; 256 x 256 only */
-#define HKX_TILE_W4 2       /* 4 waves, one a SIMD (2 x 2, 32 x 32 MFMAs); tile_n 256 */
-#define HKX_TILE_W8 3       /* 8 waves, register-staged fills, 16 x 16 MFMAs; any tile shape */
+#define HKX_TILE_W4 2       /* 4 waves, one a SIMD (2 x 2, 32 x 32 MFMAs), up to four LDS
+                               stages; 256, 128 or 64 x 256 and 128 or 64 x 128 */
+#define HKX_TILE_W8 3       /* 8 waves, register-staged fills, 16 x 16 MFMAs; every tile
+                               shape but 64 x 128 */
 #define HKX_TILE_RING 4     /* 8 waves taking turns at the MFMA, one workgroup a CU walking its
                                tiles through one LDS ring, epilogue stored from registers;
                                256 x 256 only, C rows 16-byte aligned, N % 8 == 0 */
@@ -204,7 +206,7 @@ typedef struct HkxGemmArgs {
   int32_t ab_dtype; /* HKX_BF16, HKX_FP8E4M3 (both operands), or an e5m2 pair code */
   int32_t c_dtype;  /* HKX_BF16 / HKX_FP16 / HKX_FP32 / HKX_INT8 / HKX_FP8E4M3 */
   int32_t kernel;   /* HKX_KERNEL_* */
-  int32_t tile_m;   /* TILE: 64, 128 or 256 */
+  int32_t tile_m;   /* TILE: 64, 128 or 256 (256 x 128 on W8 only, 64 x 128 on W4 only) */
   int32_t tile_n;   /* TILE: 128 or 256 */
   int32_t splits;   /* >= 1; > 1 stores fp32 shares to ws and sums them in order */
   int32_t tile_schedule; /* TILE: HKX_TILE_*; AUTO = RING for 256 x 256 tiles it takes,

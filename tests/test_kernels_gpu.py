@@ -49,7 +49,8 @@ SNAME = {PP: "pp", W4: "w4", W8: "w8", RING: "ring"}
 TILES = [(256, 256, RING, 0), (256, 256, PP, 0), (256, 256, PP, nat.PP_MFMA32),
          (256, 256, PP, nat.PP_ONE_TILE),
          (256, 256, W4, 0), (128, 256, W4, 0), (64, 256, W4, 0), (256, 256, W8, 0),
-         (128, 256, W8, 0), (64, 256, W8, 0), (128, 128, W8, 0), (256, 128, W8, 0)]
+         (128, 256, W8, 0), (64, 256, W8, 0), (128, 128, W8, 0), (256, 128, W8, 0),
+         (128, 128, W4, 0), (64, 128, W4, 0)]
 
 
 def tile_id(t):
@@ -116,7 +117,8 @@ def test_tile_out_dtypes_residual_colscale(out, sched):
 
 
 @pytest.mark.parametrize("tile", [(256, 256, RING), (256, 256, PP), (256, 256, W4), (64, 256, W4),
-                                  (256, 256, W8), (128, 128, W8)], ids=tile_id)
+                                  (256, 256, W8), (128, 128, W8), (128, 128, W4), (64, 128, W4)],
+                         ids=tile_id)
 def test_tile_fp8_scaled(tile):
     m, n, k = 300, 512, 1024
     g = torch.Generator().manual_seed(11)
@@ -138,6 +140,52 @@ def test_tile_fp8_scaled(tile):
     _run(a8.to(DEV), b8.to(DEV), c2, kernel=nat.KERNEL_TILE, tile_m=tile[0], tile_n=tile[1],
          schedule=tile[2], ep=ep)
     O.assert_close(c2, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("bm", [128, 64])
+@pytest.mark.parametrize("form", ["plain", "bias_gelu", "residual", "silu_mul", "int8", "fp32"])
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("k", [64, 192, 640])
+def test_w4_128_columns(bm, form, splits, k):
+    """The 4-wave kernel's 128-column tiles (four LDS stages): K-tile counts below, at and
+    past the stage count (1, 3, 10), split over K, ragged M and N, every store mode."""
+    m, n = 300, 520
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=bm, tile_n=128, schedule=W4, splits=splits)
+    if form == "silu_mul":
+        a, b = _data(m, 2 * n, k, seed=81)
+        acc = O.gemm_fp32(a, b)
+        c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+        ep = nat.HkxEpilogue()
+        ep.form = nat.EP_SILU_MUL
+        _run(a.to(DEV), b.to(DEV), c, ep=ep, **kw)
+        O.assert_close(c, O.silu_and_mul(acc[:, :n], acc[:, n:]), rtol=1e-2, atol=1e-2)
+        return
+    a, b = _data(m, n, k, seed=80)
+    acc = O.gemm_fp32(a, b)
+    g = torch.Generator().manual_seed(82)
+    if form == "int8":
+        sd = torch.full((n,), 40.0).to(DEV)
+        c = torch.empty((m, n), dtype=torch.int8, device=DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(sd, nat.ROW)], rs=0), **kw)
+        assert (c.cpu().float() - O.quantize_int8(acc * 40)).abs().max().item() <= 1.0
+        return
+    c = torch.full((m, n), 7.0, dtype=torch.float32 if form == "fp32" else torch.bfloat16,
+                   device=DEV)
+    if form in ("plain", "fp32"):
+        _run(a.to(DEV), b.to(DEV), c, **kw)
+        ref = acc
+    elif form == "bias_gelu":
+        bias = torch.randn(n, generator=g).to(torch.bfloat16)
+        ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
+        bd = bias.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
+    else:
+        res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+        rs = torch.rand(m, 1, generator=g) + 0.5
+        ref = acc * rs + res.float()
+        resd, rsd = res.to(DEV), rs.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(rsd, nat.COL), (resd, nat.TILE)], cs=0, ta=1), **kw)
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 32])
