@@ -19,7 +19,13 @@ int quad_form(const TileArgs& a, bool fp8, int mode) {
   if (mode == kPair16) return fp8 ? -1 : kEpNone;
   const Fused& e = a.ep;
   if (e.form == HKX_EP_NONE) return kEpNone;
-  if (e.form != HKX_EP_FUSED || e.ta.p || e.cmul != 1.0f || e.cadd != 0.0f) return -1;
+  if (e.form != HKX_EP_FUSED || e.cmul != 1.0f || e.cadd != 0.0f) return -1;
+  if (e.ta.p) {  // a bf16 tile operand of 16-byte aligned rows, whose offsets fit 32 bits
+    if (fp8 || e.cs.p || e.rs.p || e.ta.dt != HKX_BF16 || ((uintptr_t)e.ta.p & 15) ||
+        (e.ta.ld * 2) % 16 || (int64_t)((a.M + 255) / 256) * 256 * e.ta.ld * 2 >= (1LL << 32))
+      return -1;
+    return !e.ra.p || vec16_16(e.ra) ? kEpTile : -1;
+  }
   if (fp8) {
     if (e.act != HKX_ACT_NONE) return -1;
     if (!e.cs.p && !e.rs.p && !e.ra.p) return kEpNone;
@@ -65,6 +71,7 @@ hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStre
   }
   const int act = a.ep.form == HKX_EP_FUSED ? a.ep.act : HKX_ACT_NONE;
   if (epf == kEpBias) { HKX_QUAD_ACTS(kEpBias) }
+  else if (epf == kEpTile) { HKX_QUAD_ACTS(kEpTile) }
   else { HKX_QUAD_ACTS(kEpNone) }
   return hipGetLastError();
 }

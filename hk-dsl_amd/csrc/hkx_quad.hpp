@@ -62,7 +62,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   constexpr int SMEM = EPV + (MX ? 3 * 8192 : 3 * 3 * 1024);
   static_assert(!MX || (FP8 && EPF == kEpNone), "MX scales go with fp8 operands, no epilogue");
   static_assert(FP8 ? (EPF == kEpNone || EPF == kEpDeq || EPF == kEpDeqBias) && ACT == HKX_ACT_NONE
-                    : (EPF == kEpNone || EPF == kEpBias), "forms");
+                    : (EPF == kEpNone || EPF == kEpBias || EPF == kEpTile), "forms");
   static_assert(!PAIR || (!FP8 && EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
   static_assert(SMEM <= 160 * 1024, "LDS");
 
@@ -169,13 +169,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   // 2; lanes 32-63 read past the tile's 512 bytes into the slot's spare half). Three slots:
   // the DMA of tile lt + 1, at tile lt's first phase, runs while group 1 may still read
   // tile lt - 1's.
-  constexpr bool bias = EPF == kEpBias || EPF == kEpDeqBias;
+  // kEpTile: the bias is optional (absent, its DMA reads zeros from an empty buffer)
+  constexpr bool bias = EPF == kEpBias || EPF == kEpDeqBias || EPF == kEpTile;
   constexpr bool deq = EPF == kEpDeq || EPF == kEpDeqBias;
   const Fused& e = p.ep;
   const __amdgpu_buffer_rsrc_t rvec = make_rsrc(
       wave == 0 ? (deq ? e.cs.p : nullptr) : wave == 1 ? (deq ? e.rs.p : nullptr) : (bias ? e.ra.p : nullptr),
       wave == 0 ? (deq ? (uint32_t)p.M * 4u : 0u)
-                : wave == 1 ? (deq ? (uint32_t)p.N * 4u : 0u) : (bias ? (uint32_t)p.N * 2u : 0u));
+                : wave == 1 ? (deq ? (uint32_t)p.N * 4u : 0u) : (bias && e.ra.p ? (uint32_t)p.N * 2u : 0u));
   auto vec_load = [&](int lt) {
     if (wave > 2 || (wave < 2 && !deq) || (wave == 2 && !bias)) return;
     int m0, n0;
@@ -398,6 +399,28 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
           }
       return;
     }
+    // kEpTile: this lane's 128 values of the tile operand (bf16 rows of stride ta.ld, 16-byte
+    // aligned), all loaded before the first store so one memory latency covers them: for
+    // fragment (i, j, f), row 128 i + 64 grp + 16 f + rf, columns ca + 4 q and ca + 16 + 4 q
+    // (+ [0, 4)); rows past M read zeros through the buffer bound and are never stored
+    [[maybe_unused]] u32x2 tv[2][2][4][2];
+    if constexpr (EPF == kEpTile) {
+      const uint32_t tb = (uint32_t)e.ta.ld * 2u;
+      const __amdgpu_buffer_rsrc_t rt = make_rsrc(e.ta.p, (uint32_t)p.M * tb);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+              const int col = n0 + 128 * j + 32 * wc + 16 * g + 4 * q;
+              const int row = m0 + 128 * i + 64 * grp + 16 * f + rf;
+              tv[i][j][f][g] = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_raw_buffer_load_b64(rt, (uint32_t)row * tb + (uint32_t)col * 2u, 0, 0));
+            }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -410,6 +433,10 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
           if constexpr (bias) {
             va += bv[j][0];
             vb += bv[j][1];
+          }
+          if constexpr (EPF == kEpTile) {
+            va += unpack_bf16x4(tv[i][j][f][0]);
+            vb += unpack_bf16x4(tv[i][j][f][1]);
           }
           va = act4c<ACT>(0, va);
           vb = act4c<ACT>(0, vb);

@@ -70,6 +70,7 @@ constexpr int kEpBias = 1;     // act(acc + ra[n]), ra bf16
 constexpr int kEpDeq = 2;      // act(acc cs[m] rs[n]), cs and rs fp32
 constexpr int kEpDeqBias = 3;  // act(acc cs[m] rs[n] + ra[n]), cs and rs fp32, ra bf16
 constexpr int kEpGeneric = 4;  // the whole fused form with run-time types and output type
+constexpr int kEpTile = 5;     // act(acc + ra[n] + ta[m][n]), ra (optional) and ta bf16 (quadrant kernel)
 
 // FP8: 0 bf16 operands; 1 fp8 e4m3 x e4m3; 2 e5m2 x e5m2; 3 A e4m3 x B e5m2; 4 A e5m2 x B
 // e4m3 (TileArgs::ab_fmt). The scaled MFMA takes its first operand's format (here B's, as

@@ -473,7 +473,8 @@ def test_ring_wave_split(form, variant):
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["quad", "halfstage"])
-@pytest.mark.parametrize("form", ["plain", "bias", "bias_gelu", "silu", "silu_mul"])
+@pytest.mark.parametrize("form", ["plain", "bias", "bias_gelu", "silu", "silu_mul", "residual",
+                                  "bias_residual_gelu"])
 @pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 520, 128), (4096, 4352, 192),
                                  (1000, 2048, 1088), (2048, 9216, 512)])
 def test_ring_quad(form, mnk, half):
@@ -510,6 +511,19 @@ def test_ring_quad(form, mnk, half):
     elif form == "bias_gelu":
         ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
         _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
+    elif form in ("residual", "bias_residual_gelu"):
+        # the tile operand a strided view (row stride N + 8); with a bias and GELU, both
+        # added before the activation
+        room = torch.randn(m, n + 8, generator=g).to(torch.bfloat16)
+        res = room[:, :n]
+        resd = room.to(DEV)[:, :n]
+        if form == "residual":
+            ref = acc + res.float()
+            _run(a.to(DEV), b.to(DEV), c, ep=_fused([(resd, nat.TILE)], ta=0), **kw)
+        else:
+            ref = O.gelu_tanh(acc + bias.float() + res.float())
+            _run(a.to(DEV), b.to(DEV), c,
+                 ep=_fused([(bd, nat.ROW), (resd, nat.TILE)], ra=0, ta=1, act=nat.ACT_GELU_TANH), **kw)
     else:
         ref = O.silu(acc)
         _run(a.to(DEV), b.to(DEV), c, ep=_fused([], act=nat.ACT_SILU), **kw)
