@@ -57,10 +57,18 @@ static bool stream_fast(const DecodeArgs& a) {
 
 bool stream_takes(const DecodeArgs& a, int splits, bool pair) {
   const int groups = a.g_total;  // 128-element K groups
-  const bool tile_operand = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
+  // a tile operand reaches LDS by 4-byte DMA: bf16, fp16 or fp32, rows 4-byte aligned, byte
+  // offsets within 32 bits
+  const Opnd& t = a.ep.ta;
+  if (a.ep.form == HKX_EP_FUSED && t.p) {
+    const int eb = t.dt == HKX_FP32 ? 4 : 2;
+    if ((t.dt != HKX_BF16 && t.dt != HKX_FP16 && t.dt != HKX_FP32) || ((uintptr_t)t.p & 3) ||
+        (t.ld * eb) % 4 || (int64_t)a.M * t.ld * eb >= (1LL << 32))
+      return false;
+  }
   // two 16-token fragments (M 17-32) keep one buffer of partial sums, which needs two chunks
   // a block (K of 2048 and up)
-  return splits == 1 && !pair && !tile_operand && groups % 8 == 0 && groups <= 256 &&
+  return splits == 1 && !pair && groups % 8 == 0 && groups <= 256 &&
          (a.M <= 16 || (a.M <= 32 && groups >= 16));
 }
 

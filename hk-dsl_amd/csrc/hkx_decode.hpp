@@ -211,7 +211,11 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   constexpr int NPAR = MF == 1 ? 2 : 1;
   constexpr int RED = NR * CH;
   constexpr int EPV = RED + NPAR * NW * MF * 64 * 16;  // then the epilogue's vectors: [block % 3][cs, rs, ra][64 slots]
-  __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * 3 * 256];
+  // then, with the generic epilogue, the tile operand's values of a block: [block % 3][row
+  // < 32][16 columns], up to 64 bytes a row
+  constexpr int TOFF = EPV + 3 * 3 * 256;
+  constexpr int TSLOT = 32 * 64;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[TOFF + (EPF == kStreamEpGeneric ? 3 * TSLOT : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -273,11 +277,18 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const bool fused = e.form == HKX_EP_FUSED;
   const bool cs_vec = fused && e.cs.p && e.cs.ld, rs_vec = fused && e.rs.p && e.rs.ld,
              ra_vec = fused && e.ra.p && e.ra.ld;
+  // the tile operand (generic form only): a block's 16 columns of rows 0 .. M - 1, 4 bytes a
+  // lane, 8 rows an instruction (16-bit) or 4 (fp32); its rows start 4-byte aligned
+  const bool ta_on = EPF == kStreamEpGeneric && fused && e.ta.p;
+  const uint32_t ta_eb = ta_on && e.ta.dt == HKX_FP32 ? 4u : 2u;
+  const int ta_dpr = 4 * (int)ta_eb;  // dwords a row of the block
+  const int ta_rpi = 64 / ta_dpr;     // rows a DMA instruction
+  const int ta_n = ta_on ? (min(p.M, 16 * MF) + ta_rpi - 1) / ta_rpi : 0;
   const float cs_sc = (fused && e.cs.p && !e.cs.ld) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : e.cmul;
   const float rs_sc = (fused && e.rs.p && !e.rs.ld) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
   const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
   auto ep_load = [&](int j) {
-    if (wave != 0 || !(cs_vec || rs_vec || ra_vec)) return;
+    if (wave != 0 || !(cs_vec || rs_vec || ra_vec || ta_on)) return;
     const int bi = block_of(j);
     uint8_t* base = ring + EPV + (j % 3) * 768;
     if constexpr (EPF == kStreamEpFast) {
@@ -304,6 +315,18 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       load(e.cs, (int64_t)(p.M - 1) * e.cs.ld + 1, l < 16 * MF && l < p.M, (int64_t)l * e.cs.ld, base);
     if (rs_vec) load(e.rs, p.N, l < 16 && n < p.N, n, base + 256);
     if (ra_vec) load(e.ra, p.N, l < 16 && n < p.N, n, base + 512);
+    if (ta_on) {
+      const uint32_t rowb = (uint32_t)e.ta.ld * ta_eb;
+      const __amdgpu_buffer_rsrc_t rt = make_rsrc(e.ta.p, (uint32_t)p.M * rowb);
+      uint8_t* tslot = ring + TOFF + (j % 3) * TSLOT;
+      for (int r = 0; r < ta_n; ++r) {
+        const int row = r * ta_rpi + l / ta_dpr, d = l % ta_dpr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rt, (__attribute__((address_space(3))) void*)(tslot + r * 256), 4,
+            row < p.M ? (uint32_t)row * rowb + (uint32_t)bi * 16u * ta_eb + (uint32_t)d * 4u : kOut, 0,
+            0, 0);
+      }
+    }
   };
   // which half of its word a 16-bit element is in (from its address)
   auto hi_half = [](const Opnd& o, int64_t idx) {
@@ -364,9 +387,16 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
                               : cs_sc;
       const f32x4 rs = rs_vec ? vec4(eo + 64 + 4 * kq, e.rs, n) : f32x4{rs_sc, rs_sc, rs_sc, rs_sc};
       const f32x4 ra = ra_vec ? vec4(eo + 128 + 4 * kq, e.ra, n) : f32x4{ra_sc, ra_sc, ra_sc, ra_sc};
-      // (no tile operand here: stream_takes leaves those calls to decode_kernel, since its
-      // direct load would make wave 0 wait for every fill in flight)
-      sum = act4(e.act, sum * (rs * cs) + ra + e.cadd);
+      f32x4 tv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (ta_on) {  // from LDS (a direct load would make wave 0 wait for every fill in flight)
+        const uint8_t* ts = ring + TOFF + (j % 3) * TSLOT + m * ta_dpr * 4;
+        if (e.ta.dt == HKX_FP32) tv = *(const f32x4*)(ts + 16 * kq);
+        else {
+          const u32x2 w = *(const u32x2*)(ts + 8 * kq);
+          tv = e.ta.dt == HKX_FP16 ? unpack_f16x4(w) : unpack_bf16x4(w);
+        }
+      }
+      sum = act4(e.act, sum * (rs * cs) + ra + tv + e.cadd);
     }
     if (m < p.M && n < p.N) store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, sum);
     }
@@ -382,7 +412,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // f(q + 2), each 4 a wave where it exists (anything issued later only makes the wait
   // stricter); lgkmcnt(0) as well
   // wave 0's epilogue-vector DMAs of the step before (ep_load) are among them too
-  const int nvec = EPF == kStreamEpFast ? (int)ra_vec : (int)cs_vec + (int)rs_vec + (int)ra_vec;
+  const int nvec = EPF == kStreamEpFast ? (int)ra_vec : (int)cs_vec + (int)rs_vec + (int)ra_vec + ta_n;
   auto wait_chunk = [&](int q, bool ep_before) {
     const int n = 4 * ((q + 1 < nq) + (q + 2 < nq)) + 4 * MF * has_x(q + 1) + (ep_before && wave == 0 ? nvec : 0);
     switch (n) {
@@ -390,7 +420,10 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       HKX_WAIT_CASE(1) HKX_WAIT_CASE(2) HKX_WAIT_CASE(3) HKX_WAIT_CASE(4) HKX_WAIT_CASE(5)
       HKX_WAIT_CASE(6) HKX_WAIT_CASE(7) HKX_WAIT_CASE(8) HKX_WAIT_CASE(9) HKX_WAIT_CASE(10)
       HKX_WAIT_CASE(11) HKX_WAIT_CASE(12) HKX_WAIT_CASE(13) HKX_WAIT_CASE(14) HKX_WAIT_CASE(15)
-      HKX_WAIT_CASE(16) HKX_WAIT_CASE(17) HKX_WAIT_CASE(18) HKX_WAIT_CASE(19)
+      HKX_WAIT_CASE(16) HKX_WAIT_CASE(17) HKX_WAIT_CASE(18) HKX_WAIT_CASE(19) HKX_WAIT_CASE(20)
+      HKX_WAIT_CASE(21) HKX_WAIT_CASE(22) HKX_WAIT_CASE(23) HKX_WAIT_CASE(24) HKX_WAIT_CASE(25)
+      HKX_WAIT_CASE(26) HKX_WAIT_CASE(27) HKX_WAIT_CASE(28) HKX_WAIT_CASE(29) HKX_WAIT_CASE(30)
+      HKX_WAIT_CASE(31)
 #undef HKX_WAIT_CASE
       default: __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8)); break;
     }

@@ -420,6 +420,27 @@ def test_decode_stream_fused_forms(m, nk):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("m", [1, 9, 16, 24, 32])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("nk", [(1000, 2048), (4096, 12288)])
+def test_decode_stream_residual(m, dt, nk):
+    """A residual tile on the streaming decode kernel (staged through LDS by DMA a block
+    ahead, like the vector operands): 16- and 32-bit operands, a strided view (row stride
+    N + 4), X held or streamed (K = 12288)."""
+    n, k = nk
+    a, b = _data(m, n, k, seed=29)
+    g = torch.Generator().manual_seed(30)
+    acc = O.gemm_fp32(a, b)
+    room = torch.randn(m, n + 4, generator=g).to(dt)
+    res = room[:, :n]
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    resd = room.to(DEV)[:, :n]
+    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+         ep=_fused([(resd, nat.TILE)], ta=0))
+    O.assert_close(c, acc + res.float(), rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("variant", [nat.RING_WAVESPLIT, nat.RING_STREAMK], ids=["ppw", "sk"])
 @pytest.mark.parametrize("form", ["bias_gelu", "residual_colscale", "silu_mul", "fp8_deq_bias"])
 def test_ring_wave_split(form, variant):
