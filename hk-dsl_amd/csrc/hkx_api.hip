@@ -242,8 +242,13 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
     if (sc == HKX_TILE_AUTO) sc = pp_ok ? HKX_TILE_RING : (four_ok ? HKX_TILE_W4 : HKX_TILE_W8);
     if (sc != HKX_TILE_PINGPONG && sc != HKX_TILE_W4 && sc != HKX_TILE_W8 && sc != HKX_TILE_RING)
       return fail(HKX_ERR_ARG, "tile_schedule %d", a->tile_schedule);
-    if (sc == HKX_TILE_RING && !pp_ok)
-      return fail(HKX_ERR_ARG, "the ring tile kernel takes 256x256 tiles");
+    // RING at 128 x 256: the quadrant kernel's 128-row form (where it takes the call; else
+    // the 4-wave kernel), no variant bits
+    const bool q128 = bm == 128 && bn == 256;
+    if (sc == HKX_TILE_RING && !pp_ok && !q128)
+      return fail(HKX_ERR_ARG, "the ring tile kernel takes 256x256 tiles (128x256: its quadrant form)");
+    if (sc == HKX_TILE_RING && q128 && a->variant)
+      return fail(HKX_ERR_ARG, "variant %d: the 128x256 quadrant form has none", a->variant);
     if (sc == HKX_TILE_W4 && !four_ok)
       return fail(HKX_ERR_ARG, "the 4-wave tile kernel takes 256x256, 128x256, 64x256, 128x128 "
                   "or 64x128 tiles");
@@ -387,6 +392,14 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
     dim3 g = grid;
     g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
     return hkx::launch_ring(t, fp8, mode, g, s);
+  }
+  if (p.schedule == HKX_TILE_RING && bm == 128) {  // the 128-row quadrant form, or the 4-wave kernel
+    if (grid.y == 1 && hkx::quad128_takes(t, fp8, mode)) {
+      dim3 g = grid;
+      g.x = std::min<unsigned>(g.x, (unsigned)cu_count());
+      return hkx::launch_quad128(t, mode, g, s);
+    }
+    return hkx::launch_tile4<128, 256>(t, fp8, mode, grid, s);
   }
   if (p.schedule == HKX_TILE_RING && hkx::ring_takes(t, fp8, mode)) {
     dim3 g = grid;

@@ -42,6 +42,10 @@ hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 g
 // epilogue or the dequant forms (row and column fp32 scales, a bf16 bias). Vectors of unit
 // stride, 16-byte aligned; quad_takes says which calls.
 bool quad_takes(const TileArgs& a, bool fp8, int mode);
+// The quadrant kernel on 128 x 256 tiles (bf16, one phase a K-tile): the calls it takes, and
+// its launch (grid: one workgroup a CU at most).
+bool quad128_takes(const TileArgs& a, bool fp8, int mode);
+hipError_t launch_quad128(const TileArgs& a, int mode, dim3 grid, hipStream_t s);
 hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s);
 // Its MX form (fp8 operands, E8M0 block scales in a.sa / a.sb, bf16 C, one pass).
 hipError_t launch_quad_mx(const TileArgs& a, dim3 grid, hipStream_t s);

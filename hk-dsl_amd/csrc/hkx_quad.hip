@@ -44,6 +44,10 @@ bool quad_takes(const TileArgs& a, bool fp8, int mode) {
   return a.ab_fmt <= 1 && quad_form(a, fp8, mode) >= 0;
 }
 
+bool quad128_takes(const TileArgs& a, bool fp8, int mode) {
+  return !fp8 && a.ab_fmt == 0 && quad_form(a, false, mode) >= 0;
+}
+
 #define HKX_QUAD(ACT, EPF) hipLaunchKernelGGL((quad_kernel<ACT, EPF>), grid, dim3(512), 0, s, a)
 #define HKX_QUAD_ACTS(EPF)                                            \
   switch (act) {                                                      \
@@ -73,6 +77,30 @@ hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStre
   if (epf == kEpBias) { HKX_QUAD_ACTS(kEpBias) }
   else if (epf == kEpTile) { HKX_QUAD_ACTS(kEpTile) }
   else { HKX_QUAD_ACTS(kEpNone) }
+  return hipGetLastError();
+}
+
+#define HKX_QUAD128(ACT, EPF) \
+  hipLaunchKernelGGL((quad_kernel<ACT, EPF, false, false, false, 128>), grid, dim3(512), 0, s, a)
+#define HKX_QUAD128_ACTS(EPF)                                            \
+  switch (act) {                                                         \
+    case HKX_ACT_GELU_TANH: HKX_QUAD128(HKX_ACT_GELU_TANH, EPF); break; \
+    case HKX_ACT_SILU: HKX_QUAD128(HKX_ACT_SILU, EPF); break;           \
+    case HKX_ACT_RELU: HKX_QUAD128(HKX_ACT_RELU, EPF); break;           \
+    default: HKX_QUAD128(HKX_ACT_NONE, EPF); break;                    \
+  }
+
+hipError_t launch_quad128(const TileArgs& a, int mode, dim3 grid, hipStream_t s) {
+  const int epf = quad128_takes(a, false, mode) ? quad_form(a, false, mode) : -1;
+  if (epf < 0) return hipErrorInvalidValue;
+  if (mode == kPair16) {
+    hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, true, false, false, 128>), grid, dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
+  const int act = a.ep.form == HKX_EP_FUSED ? a.ep.act : HKX_ACT_NONE;
+  if (epf == kEpBias) { HKX_QUAD128_ACTS(kEpBias) }
+  else if (epf == kEpTile) { HKX_QUAD128_ACTS(kEpTile) }
+  else { HKX_QUAD128_ACTS(kEpNone) }
   return hipGetLastError();
 }
 

@@ -51,11 +51,15 @@
 
 namespace hkx {
 
-template <int ACT, int EPF, bool PAIR = false, bool FP8 = false, bool MX = false>
+template <int ACT, int EPF, bool PAIR = false, bool FP8 = false, bool MX = false, int BM = 256>
 __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
-  constexpr int BM = 256, BN = PAIR ? 128 : 256;  // BN: C columns of a tile
-  constexpr int QB = 128 * 128;       // one quarter: 128 rows x 128 bytes
-  constexpr int EPV = 8 * QB;         // then the epilogue's vectors: [tile % 3][cs, rs, ra][1 KB]
+  constexpr int BN = PAIR ? 128 : 256;  // BN: C columns of a tile
+  static_assert(BM == 256 || (BM == 128 && !FP8 && !MX), "128-row tiles: bf16 only");
+  constexpr int NI = BM / 128;          // A halves of a tile
+  constexpr int QPS = NI + 2;           // quarters a K-tile slot: the A halves, B0, B1
+  constexpr int NSL = NI == 2 ? 2 : 3;  // K-tile slots
+  constexpr int QB = 128 * 128;         // one quarter: 128 rows x 128 bytes
+  constexpr int EPV = NSL * QPS * QB;   // then the epilogue's vectors: [tile % 3][cs, rs, ra][1 KB]
   // MX: in their place, E8M0 scale chunks [chunk % 3][512 rows: A, then B][16 bytes]; a chunk
   // the scales of 4 K-tiles (16 blocks of 32 K) of every row of the tile
   constexpr int SCO = EPV;
@@ -134,13 +138,16 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       tile_at(++s.lt, s.m0, s.n0);
     }
   };
-  // quarter q (0 A0, 1 A1, 2 B0, 3 B1) of stream s's K-tile into slot g & 1
+  // quarter q (0 A0, 1 A1, 2 B0, 3 B1) of slot sl
+  auto slot_of = [](int g) { return NSL == 2 ? (g & 1) : g % NSL; };
+  auto quarter = [&](int sl, int q) { return smem + (sl * QPS + (q < 2 ? q : NI + q - 2)) * QB; };
+  // quarter q of stream s's K-tile into its slot
   auto fill = [&](int q, const Stream& s) {
     const bool isb = q >= 2;
     const uint32_t ld = isb ? p.ldb_b : p.lda_b;
     const uint32_t row0 = (uint32_t)((isb ? s.n0 : s.m0) + (isb && PAIR ? 64 : 128) * (q & 1));
     const uint32_t so = __builtin_amdgcn_readfirstlane(row0 * ld + (uint32_t)s.t * 128u);
-    uint8_t* base = smem + ((s.g & 1) * 4 + q) * QB + wave * 2048;
+    uint8_t* base = quarter(slot_of(s.g), q) + wave * 2048;
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       buf_load16_lds(isb ? rb : ra, base + k * 1024, (isb ? lrow_b[k] : lrow[k]) * ld + lch[k], so);
@@ -221,14 +228,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     }
   };
   auto read_a = [&](int slot, int i) {
-    const uint8_t* s = smem + (slot * 4 + i) * QB;
+    const uint8_t* s = quarter(slot, i);
 #pragma unroll
     for (int f = 0; f < NA; ++f)
 #pragma unroll
       for (int h = 0; h < 2; ++h) af[f][h] = frag_at(s, grp * 64 + (64 / NA) * f, h, f & 1);
   };
   auto read_b = [&](int slot, int j, Frag (&bf)[NB][2]) {
-    const uint8_t* s = smem + (slot * 4 + 2 + j) * QB;
+    const uint8_t* s = quarter(slot, 2 + j);
 #pragma unroll
     for (int g = 0; g < NB; ++g)
 #pragma unroll
@@ -253,7 +260,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   const int sc_sh = 8 * (lane >> 5);
 
   using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
-  Acc acc[2][2][NA][NB];  // [A half][B half][row fragment][column fragment]
+  Acc acc[NI][2][NA][NB];  // [A half][B half][row fragment][column fragment]
   auto math = [&](int i, int j, const Frag (&bf)[NB][2], bool zero) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -380,7 +387,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       // C: 2.9 TB/s, against 2.5 for the 8-byte stores of 16 rows x 32 bytes)
       const int n = 64 * 0 + 16 * wc + 8 * (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -403,12 +410,12 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     // aligned), all loaded before the first store so one memory latency covers them: for
     // fragment (i, j, f), row 128 i + 64 grp + 16 f + rf, columns ca + 4 q and ca + 16 + 4 q
     // (+ [0, 4)); rows past M read zeros through the buffer bound and are never stored
-    [[maybe_unused]] u32x2 tv[2][2][4][2];
+    [[maybe_unused]] u32x2 tv[NI][2][4][2];
     if constexpr (EPF == kEpTile) {
       const uint32_t tb = (uint32_t)e.ta.ld * 2u;
       const __amdgpu_buffer_rsrc_t rt = make_rsrc(e.ta.p, (uint32_t)p.M * tb);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -422,7 +429,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
             }
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int ca = 128 * j + 32 * wc;  // the block's first column
@@ -470,87 +477,134 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Without MX, phase 2 also reads B1 of the next K-tile (into the other of bf1 / bfn, the
-  // two alternating by K-tile) and B1's fill moves to phase 1, two K-tiles ahead: each phase
-  // then reads 12 fragments and issues 4 fills, where phase 1 read 16 and issued 2 (config 2
-  // 1-3% faster). Every quarter is still refilled only after both groups read it and about
-  // three phases before its first read, and the fills keep the order of their reads, so the
-  // waits stay "all but the newest 8". The MX form keeps B1 in phase 1: its scales leave
-  // no registers for the second B1 set.
-  constexpr bool B1N = !MX;
-  vec_load(0);
-  Stream s1 = stream_at(0), s2 = stream_at(0);
+  if constexpr (NI == 1) {
+    // 128-row tiles: one phase a K-tile (read A0, B0, B1; math (0, 0), (0, 1)) through three
+    // slots. Phase t fills K-tile t + 2 into the slot of K-tile t - 1, which group 0 read a
+    // phase and group 1 a barrier before; each fill lands three to four barriers ahead of its
+    // first read. A wave issues 6 fill instructions a phase, so before each barrier it waits
+    // for all but its 6 newest: those of K-tile t + 2.
+    auto sync6 = [&](bool lds) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (lds) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(6));
+      else __builtin_amdgcn_s_waitcnt(wait_vm(6));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    vec_load(0);
+    Stream s2 = stream_at(0);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {  // K-tile 0 whole, then K-tile 1 but A1, in steady-state order
-    if constexpr (B1N) fill(3, s2);
-    fill(2, s2);
-    scale_fill(s2);
-    if constexpr (!B1N) fill(3, s2);
-    fill(0, s2);
-    if (r == 0) {
+    for (int r = 0; r < 2; ++r) {  // K-tiles 0 and 1, in steady-state order
+      fill(2, s2);
+      fill(3, s2);
+      fill(0, s2);
+      advance(s2);
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm(6));  // K-tile 0
+    __builtin_amdgcn_s_barrier();
+    if (grp == 1) __builtin_amdgcn_s_barrier();
+    int g = 0;
+    for (int lt = 0; lt < my_tiles; ++lt) {
+      for (int t = 0; t < nkt; ++t, ++g) {
+        const int slot = slot_of(g);
+        const bool z = t == 0;
+        read_a(slot, 0);
+        read_b(slot, 0, bf0);
+        read_b(slot, 1, bf1);
+        if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
+        fill(2, s2);
+        fill(3, s2);
+        fill(0, s2);
+        advance(s2);
+        sync6(true);
+        math(0, 0, bf0, z);
+        math(0, 1, bf1, z);
+        sync6(false);
+      }
+      epilogue(lt);
+    }
+  } else {
+  // Without MX, phase 2 also reads B1 of the next K-tile (into the other of bf1 / bfn, the
+    // two alternating by K-tile) and B1's fill moves to phase 1, two K-tiles ahead: each phase
+    // then reads 12 fragments and issues 4 fills, where phase 1 read 16 and issued 2 (config 2
+    // 1-3% faster). Every quarter is still refilled only after both groups read it and about
+    // three phases before its first read, and the fills keep the order of their reads, so the
+    // waits stay "all but the newest 8". The MX form keeps B1 in phase 1: its scales leave
+    // no registers for the second B1 set.
+    constexpr bool B1N = !MX;
+    vec_load(0);
+    Stream s1 = stream_at(0), s2 = stream_at(0);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {  // K-tile 0 whole, then K-tile 1 but A1, in steady-state order
+      if constexpr (B1N) fill(3, s2);
+      fill(2, s2);
+      scale_fill(s2);
+      if constexpr (!B1N) fill(3, s2);
+      fill(0, s2);
+      if (r == 0) {
+        fill(1, s1);
+        advance(s1);
+      }
+      advance(s2);
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm(8));  // A0, B0 and B1 of K-tile 0
+    __builtin_amdgcn_s_barrier();
+    if constexpr (B1N) {  // B1 of K-tile 0, read by every wave before any refill of it
+      read_b(0, 1, bf1);
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
+      __builtin_amdgcn_s_barrier();
+    }
+    if (grp == 1) __builtin_amdgcn_s_barrier();
+    // K-tile t of local tile lt, the workgroup's g-th: b1 holds its B1 fragments, nb1 takes
+    // the next K-tile's (B1N)
+    auto ktile = [&](int lt, int t, int g, Frag (&b1)[NB][2], Frag (&nb1)[NB][2]) {
+      const int slot = g & 1;
+      const bool z = t == 0;
+      // phase 1
+      read_a(slot, 0);
+      read_b(slot, 0, bf0);
+      if constexpr (!B1N) read_b(slot, 1, b1);
+      read_scales(lt, t);
+      if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
       fill(1, s1);
       advance(s1);
-    }
-    advance(s2);
-  }
-  __builtin_amdgcn_s_waitcnt(wait_vm(8));  // A0, B0 and B1 of K-tile 0
-  __builtin_amdgcn_s_barrier();
-  if constexpr (B1N) {  // B1 of K-tile 0, read by every wave before any refill of it
-    read_b(0, 1, bf1);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(8));
-    __builtin_amdgcn_s_barrier();
-  }
-  if (grp == 1) __builtin_amdgcn_s_barrier();
-  // K-tile t of local tile lt, the workgroup's g-th: b1 holds its B1 fragments, nb1 takes
-  // the next K-tile's (B1N)
-  auto ktile = [&](int lt, int t, int g, Frag (&b1)[NB][2], Frag (&nb1)[NB][2]) {
-    const int slot = g & 1;
-    const bool z = t == 0;
-    // phase 1
-    read_a(slot, 0);
-    read_b(slot, 0, bf0);
-    if constexpr (!B1N) read_b(slot, 1, b1);
-    read_scales(lt, t);
-    if (t == 0 && lt + 1 < my_tiles) vec_load(lt + 1);
-    fill(1, s1);
-    advance(s1);
-    if constexpr (B1N) fill(3, s2);
-    sync_mem();
-    math(0, 0, bf0, z);
-    math(0, 1, b1, z);
-    sync_math();
-    // phase 2
-    read_a(slot, 1);
-    if constexpr (B1N) read_b(slot ^ 1, 1, nb1);
-    fill(2, s2);
-    scale_fill(s2);
-    if constexpr (!B1N) fill(3, s2);
-    fill(0, s2);
-    advance(s2);
-    sync_mem();
-    math(1, 0, bf0, z);
-    math(1, 1, b1, z);
-    sync_math();
-  };
-  int g = 0;
-  for (int lt = 0; lt < my_tiles; ++lt) {
-    if constexpr (B1N) {
-      int t = 0;
-      for (; t + 1 < nkt; t += 2, g += 2) {
-        ktile(lt, t, g, bf1, bfn);
-        ktile(lt, t + 1, g + 1, bfn, bf1);
-      }
-      if (t < nkt) {  // an odd count: the last K-tile, and the next tile's B1 back in bf1
-        ktile(lt, t, g++, bf1, bfn);
+      if constexpr (B1N) fill(3, s2);
+      sync_mem();
+      math(0, 0, bf0, z);
+      math(0, 1, b1, z);
+      sync_math();
+      // phase 2
+      read_a(slot, 1);
+      if constexpr (B1N) read_b(slot ^ 1, 1, nb1);
+      fill(2, s2);
+      scale_fill(s2);
+      if constexpr (!B1N) fill(3, s2);
+      fill(0, s2);
+      advance(s2);
+      sync_mem();
+      math(1, 0, bf0, z);
+      math(1, 1, b1, z);
+      sync_math();
+    };
+    int g = 0;
+    for (int lt = 0; lt < my_tiles; ++lt) {
+      if constexpr (B1N) {
+        int t = 0;
+        for (; t + 1 < nkt; t += 2, g += 2) {
+          ktile(lt, t, g, bf1, bfn);
+          ktile(lt, t + 1, g + 1, bfn, bf1);
+        }
+        if (t < nkt) {  // an odd count: the last K-tile, and the next tile's B1 back in bf1
+          ktile(lt, t, g++, bf1, bfn);
 #pragma unroll
-        for (int f = 0; f < NB; ++f)
+          for (int f = 0; f < NB; ++f)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) bf1[f][h] = bfn[f][h];
+            for (int h = 0; h < 2; ++h) bf1[f][h] = bfn[f][h];
+        }
+      } else {
+        for (int t = 0; t < nkt; ++t, ++g) ktile(lt, t, g, bf1, bf1);
       }
-    } else {
-      for (int t = 0; t < nkt; ++t, ++g) ktile(lt, t, g, bf1, bf1);
+      epilogue(lt);
     }
-    epilogue(lt);
   }
   if (grp == 0) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no fill lands in LDS after the exit

@@ -349,7 +349,7 @@ def gemm_candidates(m: int, n: int, k: int) -> List[str]:
                 "t64x128", "t64x128k2", "t64x128k4", "t64x128k8"]
     if 64 < m <= 2048:
         out += ["t128", "t128w8", "t128k2", "t128k4", "t256n128",
-                "t128x128", "t128x128k2", "t128x128k4"]
+                "t128x128", "t128x128k2", "t128x128k4", "q128"]
     if m >= 256:
         out += ["t256", "t256w", "t256sk", "t256k2", "t256w8"]
     return out

@@ -63,6 +63,9 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     "t64k2": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 2},
     "t64k4": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 4},
     "t64k8": {"kernel": "tile", "tile_m": 64, "tile_n": 256, "schedule": "w4", "splits": 8},
+    # 128 x 256 tiles on the quadrant kernel (8 waves in two ping-pong groups, one phase a
+    # K-tile, three LDS slots); calls it does not take run on the 4-wave kernel
+    "q128": {"kernel": "tile", "tile_m": 128, "tile_n": 256, "schedule": "ring"},
     # 128-column tiles on the 4-wave kernel (four LDS stages): twice the tiles of the
     # 256-column ones at mid M, so fewer splits fill the CUs (gemm_cdna_dp.py's dp64 / dp128
     # blocks are 128 columns wide)

@@ -50,7 +50,7 @@ TILES = [(256, 256, RING, 0), (256, 256, PP, 0), (256, 256, PP, nat.PP_MFMA32),
          (256, 256, PP, nat.PP_ONE_TILE),
          (256, 256, W4, 0), (128, 256, W4, 0), (64, 256, W4, 0), (256, 256, W8, 0),
          (128, 256, W8, 0), (64, 256, W8, 0), (128, 128, W8, 0), (256, 128, W8, 0),
-         (128, 128, W4, 0), (64, 128, W4, 0)]
+         (128, 128, W4, 0), (64, 128, W4, 0), (128, 256, RING, 0)]
 
 
 def tile_id(t):
@@ -493,7 +493,7 @@ def test_ring_wave_split(form, variant):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("half", [False, True], ids=["quad", "halfstage"])
+@pytest.mark.parametrize("half", [False, True, "q128"], ids=["quad", "halfstage", "quad128"])
 @pytest.mark.parametrize("form", ["plain", "bias", "bias_gelu", "silu", "silu_mul", "residual",
                                   "bias_residual_gelu"])
 @pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 520, 128), (4096, 4352, 192),
@@ -504,10 +504,14 @@ def test_ring_quad(form, mnk, half):
     (its fills run on into the next tile), ragged M and N, 272 tiles on 256 workgroups
     (some walk two), K-tiles past what two LDS slots hold; with wave split (the rest of N
     on 128 x 256 tiles) at 2048 x 9216; the paired silu * up form (128 C columns a tile,
-    gate and up rows N apart). Its wait counts and fill order run on K-tile counts 1-17."""
+    gate and up rows N apart). Its wait counts and fill order run on K-tile counts 1-17.
+    "quad128": the same calls on 128 x 256 tiles (one phase a K-tile, three slots)."""
     m, n, k = mnk
-    variant = (nat.RING_HALFSTAGE if half else 0) | (nat.RING_WAVESPLIT if n == 9216 else 0)
-    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, variant=variant)
+    if half == "q128":  # 128 x 256 tiles: the quadrant kernel's one-phase form
+        kw = dict(kernel=nat.KERNEL_TILE, tile_m=128, tile_n=256, schedule=RING)
+    else:
+        variant = (nat.RING_HALFSTAGE if half else 0) | (nat.RING_WAVESPLIT if n == 9216 else 0)
+        kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, variant=variant)
     if form == "silu_mul":  # B holds the gate rows, then the up rows
         a, b = _data(m, 2 * n, k, seed=62)
         acc = O.gemm_fp32(a, b)
