@@ -404,7 +404,9 @@ hipError_t tile_dispatch(const Plan& p, const hkx::TileArgs& t, bool fp8, int mo
   if (p.schedule == HKX_TILE_RING && hkx::ring_takes(t, fp8, mode)) {
     dim3 g = grid;
     g.x = std::min<unsigned>(g.x, (unsigned)std::max(1, cu_count() / (int)grid.y));
-    if (!(p.variant & HKX_RING_HALFSTAGE) && grid.y == 1 && hkx::quad_takes(t, fp8, mode))
+    // the quadrant kernel: one pass, or a K split into fp32 shares
+    if (!(p.variant & HKX_RING_HALFSTAGE) && (grid.y == 1 || mode == hkx::kStoreF32) &&
+        hkx::quad_takes(t, fp8, mode))
       return hkx::launch_quad(t, fp8, mode, g, s);
     return hkx::launch_ring(t, fp8, mode, g, s);
   }

@@ -38,9 +38,10 @@ hipError_t launch_ring(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStre
 hipError_t launch_ring_bf16(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
 hipError_t launch_ring_fp8(const TileArgs& a, int mode, int epf, int act, dim3 grid, hipStream_t s);
 // The quadrant ring kernel (hkx_quad.hpp): a 16-bit bf16 C, no split; bf16 operands with no
-// epilogue, a bias and an activation, or the paired silu * up form; fp8 operands with no
-// epilogue or the dequant forms (row and column fp32 scales, a bf16 bias). Vectors of unit
-// stride, 16-byte aligned; quad_takes says which calls.
+// epilogue, a bias and an activation, a residual tile, or the paired silu * up form; fp8
+// operands with no epilogue or the dequant forms (row and column fp32 scales, a bf16 bias).
+// Vectors of unit stride, 16-byte aligned. Or, unpaired, a K split's fp32 shares (mode
+// kStoreF32, blockIdx.y the split). quad_takes says which calls.
 bool quad_takes(const TileArgs& a, bool fp8, int mode);
 // The quadrant kernel on 128 x 256 tiles (bf16, one phase a K-tile): the calls it takes, and
 // its launch (grid: one workgroup a CU at most).

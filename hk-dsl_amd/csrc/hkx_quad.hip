@@ -13,6 +13,8 @@ bool vec32_16(const Opnd& o) { return o.p && o.dt == HKX_FP32 && o.ld == 1 && ((
 // The compiled epilogue form the quadrant kernel runs a call with, or -1 if it does not
 // take the call. Vector operands reach LDS by 16-byte DMA: unit stride, 16-byte aligned.
 int quad_form(const TileArgs& a, bool fp8, int mode) {
+  if (mode == kStoreF32)  // fp32 shares of a K split (or one fp32 sum a later pass finishes)
+    return a.c_dt == HKX_FP32 && a.ep.form == HKX_EP_NONE && ring_takes(a, fp8, mode) ? kEpNone : -1;
   if ((mode != kStore16 && mode != kPair16) || a.c_dt != HKX_BF16 || a.kt_split < a.kt_total)
     return -1;
   if (!ring_takes(a, fp8, mode)) return -1;
@@ -45,7 +47,7 @@ bool quad_takes(const TileArgs& a, bool fp8, int mode) {
 }
 
 bool quad128_takes(const TileArgs& a, bool fp8, int mode) {
-  return !fp8 && a.ab_fmt == 0 && quad_form(a, false, mode) >= 0;
+  return !fp8 && a.ab_fmt == 0 && mode != kStoreF32 && quad_form(a, false, mode) >= 0;
 }
 
 #define HKX_QUAD(ACT, EPF) hipLaunchKernelGGL((quad_kernel<ACT, EPF>), grid, dim3(512), 0, s, a)
@@ -60,6 +62,13 @@ bool quad128_takes(const TileArgs& a, bool fp8, int mode) {
 hipError_t launch_quad(const TileArgs& a, bool fp8, int mode, dim3 grid, hipStream_t s) {
   const int epf = quad_form(a, fp8, mode);
   if (epf < 0) return hipErrorInvalidValue;
+  if (mode == kStoreF32) {
+    if (fp8)
+      hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, false, true, false, 256, true>), grid, dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpNone, false, false, false, 256, true>), grid, dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   if (fp8) {
     if (epf == kEpDeqBias)
       hipLaunchKernelGGL((quad_kernel<HKX_ACT_NONE, kEpDeqBias, false, true>), grid, dim3(512), 0, s, a);

@@ -51,10 +51,15 @@
 
 namespace hkx {
 
-template <int ACT, int EPF, bool PAIR = false, bool FP8 = false, bool MX = false, int BM = 256>
+template <int ACT, int EPF, bool PAIR = false, bool FP8 = false, bool MX = false, int BM = 256,
+          bool SHARE = false>
 __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   constexpr int BN = PAIR ? 128 : 256;  // BN: C columns of a tile
   static_assert(BM == 256 || (BM == 128 && !FP8 && !MX), "128-row tiles: bf16 only");
+  // SHARE: K split over blockIdx.y, each split's fp32 sums stored as they are (a later pass
+  // adds the splits in order and applies the epilogue)
+  static_assert(!SHARE || (BM == 256 && !PAIR && !MX && EPF == kEpNone && ACT == HKX_ACT_NONE),
+                "fp32 shares: 256-row tiles, unpaired, no epilogue");
   constexpr int NI = BM / 128;          // A halves of a tile
   constexpr int QPS = NI + 2;           // quarters a K-tile slot: the A halves, B0, B1
   constexpr int NSL = NI == 2 ? 2 : 3;  // K-tile slots
@@ -81,7 +86,8 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   const int total = p.tiles_m * p.tiles_n;
   const int G = gridDim.x;
   const int my_tiles = (total - (int)blockIdx.x + G - 1) / G;
-  const int nkt = p.kt_total;     // K-tiles of 64 a tile
+  const int kt0 = SHARE ? (int)blockIdx.y * p.kt_split : 0;  // this split's first K-tile
+  const int nkt = SHARE ? min(p.kt_split, p.kt_total - kt0) : p.kt_total;  // K-tiles a tile
   const int nu = my_tiles * nkt;  // K-tiles of this workgroup
 
   // tile (m0, n0) of local tile lt: the ring kernel's XCD-chunked grouped raster
@@ -146,7 +152,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     const bool isb = q >= 2;
     const uint32_t ld = isb ? p.ldb_b : p.lda_b;
     const uint32_t row0 = (uint32_t)((isb ? s.n0 : s.m0) + (isb && PAIR ? 64 : 128) * (q & 1));
-    const uint32_t so = __builtin_amdgcn_readfirstlane(row0 * ld + (uint32_t)s.t * 128u);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(row0 * ld + (uint32_t)(kt0 + s.t) * 128u);
     uint8_t* base = quarter(slot_of(s.g), q) + wave * 2048;
 #pragma unroll
     for (int k = 0; k < 2; ++k)
@@ -287,12 +293,48 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   // q = l / 16) holds columns 4 q + [0, 4) of each 16-column fragment; the two fragments
   // of a 32-column block trade quarters (v_permlane16_swap) so each lane stores 16
   // contiguous bytes.
-  const uint32_t row_b = (uint32_t)p.ldc * 2u;
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c, (uint32_t)p.M * row_b);
+  const uint32_t row_b = (uint32_t)p.ldc * (SHARE ? 4u : 2u);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(
+      SHARE ? (const void*)((const float*)p.c + (int64_t)blockIdx.y * p.split_stride) : p.c,
+      (uint32_t)p.M * row_b);
   auto epilogue = [&](int lt) {
     int m0, n0;
     tile_at(lt, m0, n0);
     const uint8_t* ev = smem + EPV + (lt % 3) * 3072;  // cs, rs, ra
+    if constexpr (SHARE) {
+      // the split's fp32 sums, 16 bytes a lane: bf16 (16 x 16 fragments) lane (rf, q) holds
+      // row rf, columns 4 q + [0, 4) of each fragment; fp8 (32 x 32) lane (rf, h) holds row
+      // rf, columns 8 g + 4 h + [0, 4) of run g
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int f = 0; f < NA; ++f)
+#pragma unroll
+            for (int g = 0; g < NB; ++g) {
+              __builtin_amdgcn_sched_barrier(0);
+              if constexpr (FP8) {
+                const int ml = 128 * i + 64 * grp + 32 * f + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int n = n0 + 128 * j + 32 * wc + 8 * r + 4 * (lane >> 5);
+                  const Acc& a = acc[i][j][f][g];
+                  if (n < p.N)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(i32x4, f32x4{a[4 * r], a[4 * r + 1], a[4 * r + 2], a[4 * r + 3]}),
+                        rc, (uint32_t)(m0 + ml) * row_b + (uint32_t)n * 4u, 0, 0);
+                }
+              } else {
+                const int ml = 128 * i + 64 * grp + 16 * f + (lane & 15);
+                const int n = n0 + 128 * j + 32 * wc + 16 * g + 4 * (lane >> 4);
+                if (n < p.N)
+                  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j][f][g]), rc,
+                                                         (uint32_t)(m0 + ml) * row_b + (uint32_t)n * 4u, 0, 0);
+              }
+            }
+      return;
+    }
     if constexpr (FP8) {
       // 32 x 32: lane l (row l % 32, half h = l / 32) holds columns 8 g + 4 h + [0, 4) in
       // run g of a fragment's 16 values; runs 2 t and 2 t + 1 trade halves

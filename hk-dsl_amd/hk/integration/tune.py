@@ -352,6 +352,8 @@ def gemm_candidates(m: int, n: int, k: int) -> List[str]:
                 "t128x128", "t128x128k2", "t128x128k4", "q128"]
     if m >= 256:
         out += ["t256", "t256w", "t256sk", "t256k2", "t256w8"]
+    if 256 <= m <= 2048:
+        out += ["t256k4", "t256k8"]
     return out
 
 

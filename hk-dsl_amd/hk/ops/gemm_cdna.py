@@ -52,6 +52,8 @@ CANDIDATES: Dict[str, Dict[str, Any]] = {
     "t256n128": {"kernel": "tile", "tile_m": 256, "tile_n": 128, "schedule": "w8"},
     # split over K
     "t256k2": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "splits": 2},
+    "t256k4": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "splits": 4},
+    "t256k8": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "splits": 8},
     # wave split: the columns whose 256 x 256 tiles fill whole waves of the CUs on the ring
     # kernel, the rest of N on 128 x 256 tiles (gemm_cdna.py:834-835's ppw)
     "t256w": {"kernel": "tile", "tile_m": 256, "tile_n": 256, "schedule": "ring", "variant": 4},

@@ -555,6 +555,47 @@ def test_ring_quad(form, mnk, half):
     O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("splits", [2, 3, 4])
+@pytest.mark.parametrize("form", ["plain", "bias_gelu", "residual", "fp8_deq_bias"])
+def test_quad_split_k(form, splits):
+    """The quadrant kernel split over K (blockIdx.y the split, fp32 shares summed in split
+    order by the reduction, which applies the epilogue): 17 bf16 or 9 fp8 K-tiles, so the
+    last split is short; ragged M and N."""
+    m, n = 300, 520
+    kw = dict(kernel=nat.KERNEL_TILE, tile_m=256, tile_n=256, schedule=RING, splits=splits)
+    g = torch.Generator().manual_seed(90)
+    c = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    if form == "fp8_deq_bias":
+        k = 9 * 128
+        a8 = (torch.randn(m, k, generator=g) * 2).to(torch.float8_e4m3fn)
+        b8 = (torch.randn(n, k, generator=g) * 2).to(torch.float8_e4m3fn)
+        sa = (torch.rand(m, 1, generator=g) + 0.5) / 448
+        sb = (torch.rand(n, generator=g) + 0.5) / 448
+        bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+        sad, sbd, bd = sa.to(DEV), sb.to(DEV), bias.to(DEV)
+        _run(a8.to(DEV), b8.to(DEV), c,
+             ep=_fused([(sad, nat.COL), (sbd, nat.ROW), (bd, nat.ROW)], cs=0, rs=1, ra=2), **kw)
+        O.assert_close(c, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+        return
+    k = 17 * 64
+    a, b = _data(m, n, k, seed=91)
+    acc = O.gemm_fp32(a, b)
+    if form == "plain":
+        _run(a.to(DEV), b.to(DEV), c, **kw)
+        ref = acc
+    elif form == "bias_gelu":
+        bias = torch.randn(n, generator=g).to(torch.bfloat16)
+        bd = bias.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
+        ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
+    else:
+        res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+        resd = res.to(DEV)
+        _run(a.to(DEV), b.to(DEV), c, ep=_fused([(resd, nat.TILE)], ta=0), **kw)
+        ref = acc + res.float()
+    O.assert_close(c, ref, rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("half", [False, True], ids=["quad", "halfstage"])
 @pytest.mark.parametrize("form", ["plain", "deq", "deq_bias"])
 @pytest.mark.parametrize("mnk", [(256, 256, 128), (300, 520, 256), (4096, 4352, 384),
