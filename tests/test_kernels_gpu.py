@@ -537,9 +537,10 @@ def test_ring_quad(form, mnk, half):
         ref = O.apply_epilogue("bias_gelu", acc, bias=bias)
         _run(a.to(DEV), b.to(DEV), c, ep=_fused([(bd, nat.ROW)], ra=0, act=nat.ACT_GELU_TANH), **kw)
     elif form in ("residual", "bias_residual_gelu"):
-        # the tile operand a strided view (row stride N + 8); with a bias and GELU, both
-        # added before the activation
-        room = torch.randn(m, n + 8, generator=g).to(torch.bfloat16)
+        # the tile operand a strided view: row stride N + 8 (16-byte aligned rows: the
+        # quadrant kernel's form), or N + 4 with a bias and GELU (8-byte aligned rows: the
+        # quadrant kernel declines, the ring kernel's generic form runs)
+        room = torch.randn(m, n + (8 if form == "residual" else 4), generator=g).to(torch.bfloat16)
         res = room[:, :n]
         resd = room.to(DEV)[:, :n]
         if form == "residual":
