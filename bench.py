@@ -1,6 +1,7 @@
 """Benchmark of the GEMM-with-fused-epilogue path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--copy-probe]
+    python bench.py --ref-table
 
 A step is one call of hk.templates.gemm on BASELINE.json's config 2 -- the workload its
 metric is quoted on: x bf16[4096, 4096] ~N(0,1), w bf16[4096 (K), 12288 (N)] ~N(0, 0.02)
@@ -20,6 +21,9 @@ weight copies rotated past the 256 MB Infinity Cache; kernel time from a replaye
 since a ~20 us launch is shorter than the host's per-call overhead) and the fp8 scaled
 GEMM. Before the warmup steps, each workload runs untimed for a quarter of a second: the
 GPU's clocks settle only after tens of milliseconds of load.
+
+`--ref-table` instead times the 48 calls of the reference's published template table (see
+ref_table) and prints one JSON line with this build's time beside the reference's for each.
 """
 
 from __future__ import annotations
@@ -142,6 +146,136 @@ def cpu_baseline(x, wt, b):
                       f"median of 3 runs, {t:.2f} s each"}
 
 
+#: The reference's published device times of hk.templates.gemm on MI355X, µs: (layer,
+#: N, K, M, epilogue, time) -- the "template" column of docs/templates/gemm.md:273-324
+#: (Qwen3-8B's and Llama-3-8B's linear layers; bias + GELU(tanh) and a residual add; a
+#: replayed graph of the calls). Data only, compared against in ref_table.
+REF_TABLE = [
+    ('qwen3-8b o_proj', 4096, 4096, 16, 'bias_gelu', 9.1),
+    ('qwen3-8b o_proj', 4096, 4096, 128, 'bias_gelu', 14.5),
+    ('qwen3-8b o_proj', 4096, 4096, 1024, 'bias_gelu', 37.3),
+    ('qwen3-8b o_proj', 4096, 4096, 4096, 'bias_gelu', 99.1),
+    ('qwen3-8b down', 4096, 12288, 16, 'bias_gelu', 19.3),
+    ('qwen3-8b down', 4096, 12288, 128, 'bias_gelu', 27.7),
+    ('qwen3-8b down', 4096, 12288, 1024, 'bias_gelu', 88.7),
+    ('qwen3-8b down', 4096, 12288, 4096, 'bias_gelu', 266.2),
+    ('llama3-8b down', 4096, 14336, 16, 'bias_gelu', 21.4),
+    ('llama3-8b down', 4096, 14336, 128, 'bias_gelu', 29.9),
+    ('llama3-8b down', 4096, 14336, 1024, 'bias_gelu', 99.3),
+    ('llama3-8b down', 4096, 14336, 4096, 'bias_gelu', 311.5),
+    ('qwen3-8b qkv', 6144, 4096, 16, 'bias_gelu', 12.3),
+    ('qwen3-8b qkv', 6144, 4096, 128, 'bias_gelu', 18.2),
+    ('qwen3-8b qkv', 6144, 4096, 1024, 'bias_gelu', 57.2),
+    ('qwen3-8b qkv', 6144, 4096, 4096, 'bias_gelu', 155.0),
+    ('qwen3-8b gate_up', 24576, 4096, 16, 'bias_gelu', 36.7),
+    ('qwen3-8b gate_up', 24576, 4096, 128, 'bias_gelu', 35.2),
+    ('qwen3-8b gate_up', 24576, 4096, 1024, 'bias_gelu', 175.1),
+    ('qwen3-8b gate_up', 24576, 4096, 4096, 'bias_gelu', 595.0),
+    ('llama3-8b gate_up', 28672, 4096, 16, 'bias_gelu', 34.5),
+    ('llama3-8b gate_up', 28672, 4096, 128, 'bias_gelu', 40.6),
+    ('llama3-8b gate_up', 28672, 4096, 1024, 'bias_gelu', 197.6),
+    ('llama3-8b gate_up', 28672, 4096, 4096, 'bias_gelu', 697.6),
+    ('qwen3-8b o_proj', 4096, 4096, 16, 'residual', 9.1),
+    ('qwen3-8b o_proj', 4096, 4096, 128, 'residual', 14.6),
+    ('qwen3-8b o_proj', 4096, 4096, 1024, 'residual', 39.5),
+    ('qwen3-8b o_proj', 4096, 4096, 4096, 'residual', 98.4),
+    ('qwen3-8b down', 4096, 12288, 16, 'residual', 19.2),
+    ('qwen3-8b down', 4096, 12288, 128, 'residual', 27.9),
+    ('qwen3-8b down', 4096, 12288, 1024, 'residual', 90.3),
+    ('qwen3-8b down', 4096, 12288, 4096, 'residual', 264.5),
+    ('llama3-8b down', 4096, 14336, 16, 'residual', 21.4),
+    ('llama3-8b down', 4096, 14336, 128, 'residual', 30.1),
+    ('llama3-8b down', 4096, 14336, 1024, 'residual', 100.3),
+    ('llama3-8b down', 4096, 14336, 4096, 'residual', 315.6),
+    ('qwen3-8b qkv', 6144, 4096, 16, 'residual', 12.3),
+    ('qwen3-8b qkv', 6144, 4096, 128, 'residual', 18.3),
+    ('qwen3-8b qkv', 6144, 4096, 1024, 'residual', 57.6),
+    ('qwen3-8b qkv', 6144, 4096, 4096, 'residual', 155.1),
+    ('qwen3-8b gate_up', 24576, 4096, 16, 'residual', 36.0),
+    ('qwen3-8b gate_up', 24576, 4096, 128, 'residual', 35.3),
+    ('qwen3-8b gate_up', 24576, 4096, 1024, 'residual', 178.7),
+    ('qwen3-8b gate_up', 24576, 4096, 4096, 'residual', 597.9),
+    ('llama3-8b gate_up', 28672, 4096, 16, 'residual', 34.1),
+    ('llama3-8b gate_up', 28672, 4096, 128, 'residual', 40.4),
+    ('llama3-8b gate_up', 28672, 4096, 1024, 'residual', 200.0),
+    ('llama3-8b gate_up', 28672, 4096, 4096, 'residual', 703.0),
+]
+
+
+def ref_table():
+    """hk.templates.gemm on each REF_TABLE call, as the reference timed it (a graph of 16
+    calls replayed, the median of 15 replays a call): with one weight copy ("hot", as a
+    replay of the same calls reads it) and with four copies rotated past the 256 MB
+    Infinity Cache ("cold"). Each call is checked against the fp32 result first."""
+    import torch
+
+    import hk
+
+    T = hk.templates.gemm
+    dev = "cuda:0"
+    g = torch.Generator().manual_seed(0)
+
+    def graph_us(calls):
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for c in calls[:3]:
+                c()
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for c in calls:
+                c()
+        for _ in range(3):
+            gr.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(15):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            gr.replay()
+            e.record()
+            e.synchronize()
+            ts.append(s.elapsed_time(e) * 1e3 / len(calls))
+        return statistics.median(ts)
+
+    rows, weights = [], {}
+    for layer, n, k, m, ep, ref_us in REF_TABLE:
+        if (n, k) not in weights:
+            weights.clear()
+            torch.cuda.empty_cache()
+            weights[(n, k)] = [(torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+                               for _ in range(4)]
+        ws = weights[(n, k)]
+        x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(dev)
+        b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+        r = torch.randn(m, n, generator=g).to(torch.bfloat16).to(dev)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+        def call(w, ep=ep, x=x, b=b, r=r, y=y):
+            if ep == "bias_gelu":
+                T(x, w, epilogue=T.bias_gelu, bias=b, out=y)
+            else:
+                T(x, w, epilogue=T.residual, residual=r, out=y)
+
+        call(ws[0])
+        acc = x.float() @ ws[0].float().t()
+        want = (torch.nn.functional.gelu(acc + b.float(), approximate="tanh") if ep == "bias_gelu"
+                else acc + r.float())
+        torch.testing.assert_close(y.float(), want, rtol=1e-2, atol=4e-2)
+        hot = graph_us([lambda: call(ws[0]) for _ in range(16)])
+        cold = graph_us([lambda i=i: call(ws[i % 4]) for i in range(16)])
+        rows.append({"layer": layer, "N": n, "K": k, "M": m, "epilogue": ep,
+                     "reference_us": ref_us, "hot_us": round(hot, 2), "cold_us": round(cold, 2),
+                     "reference_over_hot": round(ref_us / hot, 3)})
+    under = sum(1 for x in rows if x["hot_us"] <= x["reference_us"])
+    within10 = sum(1 for x in rows if x["reference_over_hot"] >= 0.9)
+    print(json.dumps({"ref_table": "docs/templates/gemm.md:273-324 (reference, template column)",
+                      "calls": len(rows), "at_or_under_reference": under,
+                      "within_10pct": within10, "rows": rows}))
+
+
 def main():
     global RAMP_S
     ap = argparse.ArgumentParser()
@@ -153,8 +287,13 @@ def main():
                     help="seconds of untimed work before the warmup steps (0 under a profiler)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (the scale of rocprof's FETCH/WRITE_SIZE)")
+    ap.add_argument("--ref-table", action="store_true",
+                    help="time the reference's published template table instead (one JSON line)")
     args = ap.parse_args()
     RAMP_S = args.ramp
+    if args.ref_table:
+        ref_table()
+        return
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not measured "
               f"(the GEMM shards over M or N with no exchange, or over K with one all-reduce "
