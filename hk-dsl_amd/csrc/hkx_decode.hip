@@ -43,13 +43,14 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
   return launch_fn<16>(a, fn, mf, mode, grid, s);
 }
 
-// Whether the stream kernel's fast epilogue form takes the call's epilogue: no tile or
-// vector scales (broadcast ones are fine), a bias -- if any -- bf16 of unit stride, 4-byte
-// aligned, N even.
+// Whether the stream kernel's fast epilogue form takes the call's epilogue: no vector
+// scales (broadcast ones are fine), a bias -- if any -- bf16 of unit stride, 4-byte
+// aligned, N even; a tile operand -- if any -- bf16 with 16-byte aligned rows.
 static bool stream_fast(const DecodeArgs& a) {
   const Fused& e = a.ep;
   if (e.form != HKX_EP_FUSED) return true;
-  if ((e.cs.p && e.cs.ld) || (e.rs.p && e.rs.ld) || e.ta.p) return false;
+  if ((e.cs.p && e.cs.ld) || (e.rs.p && e.rs.ld)) return false;
+  if (e.ta.p && (e.ta.dt != HKX_BF16 || ((uintptr_t)e.ta.p & 15) || (e.ta.ld * 2) % 16)) return false;
   if (e.ra.p && e.ra.ld)
     return e.ra.dt == HKX_BF16 && e.ra.ld == 1 && ((uintptr_t)e.ra.p & 3) == 0 && a.N % 2 == 0;
   return true;

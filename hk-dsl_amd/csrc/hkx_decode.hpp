@@ -211,11 +211,11 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   constexpr int NPAR = MF == 1 ? 2 : 1;
   constexpr int RED = NR * CH;
   constexpr int EPV = RED + NPAR * NW * MF * 64 * 16;  // then the epilogue's vectors: [block % 3][cs, rs, ra][64 slots]
-  // then, with the generic epilogue, the tile operand's values of a block: [block % 3][row
-  // < 32][16 columns], up to 64 bytes a row
+  // then the tile operand's values of a block: [block % 3][row < 32][16 columns], up to 64
+  // bytes a row
   constexpr int TOFF = EPV + 3 * 3 * 256;
   constexpr int TSLOT = 32 * 64;
-  __shared__ __attribute__((aligned(16))) uint8_t ring[TOFF + (EPF == kStreamEpGeneric ? 3 * TSLOT : 0)];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[TOFF + 3 * TSLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -277,12 +277,16 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   const bool fused = e.form == HKX_EP_FUSED;
   const bool cs_vec = fused && e.cs.p && e.cs.ld, rs_vec = fused && e.rs.p && e.rs.ld,
              ra_vec = fused && e.ra.p && e.ra.ld;
-  // the tile operand (generic form only): a block's 16 columns of rows 0 .. M - 1, 4 bytes a
-  // lane, 8 rows an instruction (16-bit) or 4 (fp32); its rows start 4-byte aligned
-  const bool ta_on = EPF == kStreamEpGeneric && fused && e.ta.p;
+  // the tile operand (generic form only): a block's 16 columns of rows 0 .. M - 1 (32 or 64
+  // bytes a row), by 16-byte DMA where its rows start 16-byte aligned (32 or 16 rows an
+  // instruction), else by 4-byte DMA (8 or 4 rows an instruction)
+  const bool ta_on = fused && e.ta.p;
   const uint32_t ta_eb = ta_on && e.ta.dt == HKX_FP32 ? 4u : 2u;
   const int ta_dpr = 4 * (int)ta_eb;  // dwords a row of the block
-  const int ta_rpi = 64 / ta_dpr;     // rows a DMA instruction
+  const bool ta_w16 = ta_on && ((uintptr_t)e.ta.p & 15) == 0 && (e.ta.ld * ta_eb) % 16 == 0;
+  const int ta_pb = ta_w16 ? 16 : 4;               // bytes a lane moves
+  const int ta_ppr = ta_dpr * 4 / ta_pb;           // lanes a row
+  const int ta_rpi = 64 / ta_ppr;                  // rows a DMA instruction
   const int ta_n = ta_on ? (min(p.M, 16 * MF) + ta_rpi - 1) / ta_rpi : 0;
   const float cs_sc = (fused && e.cs.p && !e.cs.ld) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : e.cmul;
   const float rs_sc = (fused && e.rs.p && !e.rs.ld) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
@@ -291,15 +295,31 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     if (wave != 0 || !(cs_vec || rs_vec || ra_vec || ta_on)) return;
     const int bi = block_of(j);
     uint8_t* base = ring + EPV + (j % 3) * 768;
-    if constexpr (EPF == kStreamEpFast) {
-      // the block's 16 bf16 bias values: 8 lanes of one dword each, contiguous in LDS
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          make_rsrc(e.ra.p, (uint32_t)p.N * 2u), (__attribute__((address_space(3))) void*)(base + 512), 4,
-          lane < 8 ? (uint32_t)(bi * 32 + 4 * lane) : 0x7fffffffu, 0, 0, 0);
-      return;
-    }
     const int l = lane;
     constexpr uint32_t kOut = 0x7fffffffu;  // past every buffer's end: reads nothing
+    // the tile operand's rows of the block into its slot
+    auto tile_load = [&]() {
+      const uint32_t rowb = (uint32_t)e.ta.ld * ta_eb;
+      const __amdgpu_buffer_rsrc_t rt = make_rsrc(e.ta.p, (uint32_t)p.M * rowb);
+      uint8_t* tslot = ring + TOFF + (j % 3) * TSLOT;
+      for (int r = 0; r < ta_n; ++r) {
+        const int row = r * ta_rpi + l / ta_ppr, d = l % ta_ppr;
+        const uint32_t off =
+            row < p.M ? (uint32_t)row * rowb + (uint32_t)bi * 16u * ta_eb + (uint32_t)(d * ta_pb) : kOut;
+        auto* dst = (__attribute__((address_space(3))) void*)(tslot + r * ta_rpi * ta_dpr * 4);
+        if (ta_w16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, dst, 16, off, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, dst, 4, off, 0, 0, 0);
+      }
+    };
+    if constexpr (EPF == kStreamEpFast) {
+      // the block's 16 bf16 bias values: 8 lanes of one dword each, contiguous in LDS
+      if (ra_vec)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            make_rsrc(e.ra.p, (uint32_t)p.N * 2u), (__attribute__((address_space(3))) void*)(base + 512), 4,
+            lane < 8 ? (uint32_t)(bi * 32 + 4 * lane) : 0x7fffffffu, 0, 0, 0);
+      if (ta_on) tile_load();
+      return;
+    }
     // the word of element idx, from the operand's address rounded down to 4 bytes (the
     // bound rounded up: a dword only partly inside a buffer reads as zero)
     auto load = [&](const Opnd& o, int64_t elems, bool ok, int64_t idx, uint8_t* dst) {
@@ -315,18 +335,7 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       load(e.cs, (int64_t)(p.M - 1) * e.cs.ld + 1, l < 16 * MF && l < p.M, (int64_t)l * e.cs.ld, base);
     if (rs_vec) load(e.rs, p.N, l < 16 && n < p.N, n, base + 256);
     if (ra_vec) load(e.ra, p.N, l < 16 && n < p.N, n, base + 512);
-    if (ta_on) {
-      const uint32_t rowb = (uint32_t)e.ta.ld * ta_eb;
-      const __amdgpu_buffer_rsrc_t rt = make_rsrc(e.ta.p, (uint32_t)p.M * rowb);
-      uint8_t* tslot = ring + TOFF + (j % 3) * TSLOT;
-      for (int r = 0; r < ta_n; ++r) {
-        const int row = r * ta_rpi + l / ta_dpr, d = l % ta_dpr;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rt, (__attribute__((address_space(3))) void*)(tslot + r * 256), 4,
-            row < p.M ? (uint32_t)row * rowb + (uint32_t)bi * 16u * ta_eb + (uint32_t)d * 4u : kOut, 0,
-            0, 0);
-      }
-    }
+    if (ta_on) tile_load();
   };
   // which half of its word a 16-bit element is in (from its address)
   auto hi_half = [](const Opnd& o, int64_t idx) {
@@ -380,7 +389,10 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
       const f32x4 ra = ra_vec ? unpack_bf16x4(*(const u32x2*)(eo + 512 + 8 * kq))
                               : f32x4{ra_sc, ra_sc, ra_sc, ra_sc};
       const float sc = cs_sc * rs_sc;
-      sum = act4(e.act, sum * f32x4{sc, sc, sc, sc} + ra + e.cadd);
+      // (the fast form's tile operand is bf16, 32 bytes a row of the block)
+      const f32x4 tv = ta_on ? unpack_bf16x4(*(const u32x2*)(ring + TOFF + (j % 3) * TSLOT + m * 32 + 8 * kq))
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+      sum = act4(e.act, sum * f32x4{sc, sc, sc, sc} + ra + tv + e.cadd);
     } else if (fused) {
       const uint32_t* eo = (const uint32_t*)(ring + EPV + (j % 3) * 768);
       const float cs = cs_vec ? word_val(eo[m], e.cs.dt, hi_half(e.cs, (int64_t)m * e.cs.ld)) * e.cmul
@@ -412,7 +424,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // f(q + 2), each 4 a wave where it exists (anything issued later only makes the wait
   // stricter); lgkmcnt(0) as well
   // wave 0's epilogue-vector DMAs of the step before (ep_load) are among them too
-  const int nvec = EPF == kStreamEpFast ? (int)ra_vec : (int)cs_vec + (int)rs_vec + (int)ra_vec + ta_n;
+  const int nvec = EPF == kStreamEpFast ? (int)ra_vec + ta_n
+                                        : (int)cs_vec + (int)rs_vec + (int)ra_vec + ta_n;
   auto wait_chunk = [&](int q, bool ep_before) {
     const int n = 4 * ((q + 1 < nq) + (q + 2 < nq)) + 4 * MF * has_x(q + 1) + (ep_before && wave == 0 ? nvec : 0);
     switch (n) {

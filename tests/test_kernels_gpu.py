@@ -432,13 +432,23 @@ def test_decode_stream_residual(m, dt, nk):
     a, b = _data(m, n, k, seed=29)
     g = torch.Generator().manual_seed(30)
     acc = O.gemm_fp32(a, b)
-    room = torch.randn(m, n + 4, generator=g).to(dt)
-    res = room[:, :n]
-    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
-    resd = room.to(DEV)[:, :n]
-    _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
-         ep=_fused([(resd, nat.TILE)], ta=0))
-    O.assert_close(c, acc + res.float(), rtol=1e-2, atol=1e-2)
+    # row stride N + 4: 8-byte aligned 16-bit rows (the generic epilogue form, 4-byte DMA);
+    # bf16 also with N + 8 (16-byte aligned rows: the fast form), alone and with a bias
+    for extra, with_bias in ((4, False),) + (((8, False), (8, True)) if dt == torch.bfloat16 else ()):
+        room = torch.randn(m, n + extra, generator=g).to(dt)
+        res = room[:, :n]
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        resd = room.to(DEV)[:, :n]
+        if with_bias:
+            bias = torch.randn(n, generator=g).to(torch.bfloat16)
+            bd = bias.to(DEV)
+            _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+                 ep=_fused([(bd, nat.ROW), (resd, nat.TILE)], ra=0, ta=1))
+            O.assert_close(c, acc + bias.float() + res.float(), rtol=1e-2, atol=1e-2)
+        else:
+            _run(a.to(DEV), b.to(DEV), c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+                 ep=_fused([(resd, nat.TILE)], ta=0))
+            O.assert_close(c, acc + res.float(), rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("variant", [nat.RING_WAVESPLIT, nat.RING_STREAMK], ids=["ppw", "sk"])
