@@ -297,7 +297,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not measured "
               f"(the GEMM shards over M or N with no exchange, or over K with one all-reduce "
-              f"before the epilogue -- see DESIGN.md)", file=sys.stderr)
+              f"before the epilogue)", file=sys.stderr)
         sys.exit(2)
 
     import torch
