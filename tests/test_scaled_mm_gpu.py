@@ -75,3 +75,15 @@ def test_e5m2_needs_the_ring_kernels_n():
     a8, b8, sa, sb, _ = _ops(64, 260, 256, E5, E5, seed=15)
     with pytest.raises(hk._native.HkxError, match="ring kernel"):
         hk.ops.scaled_mm(a8.to(DEV), b8.to(DEV), sa.to(DEV), sb.to(DEV))
+
+
+@pytest.mark.parametrize("m,n,k,route", [(128, 4096, 4096, "t64x128k2"), (64, 1024, 8192, "t64x128k4")])
+def test_mid_m_splits_over_k(m, n, k, route):
+    # fp8 takes the route rule; at these shapes it splits 64 x 128 tiles over K (fp32
+    # shares summed in split order, then the dequant and the bias)
+    from hk.ops import gemm_cdna
+
+    assert gemm_cdna.route(m, n, k, fp8=True) == route
+    a8, b8, sa, sb, bias = _ops(m, n, k, E4, E4, seed=m + k)
+    got = hk.ops.scaled_mm(a8.to(DEV), b8.to(DEV), sa.to(DEV), sb.to(DEV), bias=bias.to(DEV))
+    O.assert_close(got, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
