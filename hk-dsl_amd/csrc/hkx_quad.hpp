@@ -249,8 +249,11 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   };
 
   // MX: the E8M0 dword of each of this lane's fragment rows for the K-tile (its 4 blocks,
-  // byte 2 s + h for K-half s and lane half h), read at the K-tile's first phase
+  // byte 2 s + h for K-half s and lane half h), read at the K-tile's first phase and shifted
+  // down a byte in lane half 1, so K-half s's scale is byte 2 s in every lane: the MFMA
+  // takes it by its byte select (op_sel), with no shift per MFMA
   [[maybe_unused]] uint32_t sca[2][2], scb[2];  // [A half][fragment], [B half]
+  const int sc_sh = 8 * (lane >> 5);
   auto read_scales = [&](int lt, int t) {
     if constexpr (MX) {
       const uint32_t* sc = (const uint32_t*)(smem + SCO + ((lt * cpt + (t >> 2)) % 3) * 8192) + (t & 3);
@@ -258,12 +261,11 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int f = 0; f < 2; ++f) sca[i][f] = sc[4 * (128 * i + 64 * grp + 32 * f + rf)];
+        for (int f = 0; f < 2; ++f) sca[i][f] = sc[4 * (128 * i + 64 * grp + 32 * f + rf)] >> sc_sh;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) scb[j] = sc[4 * (256 + 128 * j + 32 * wc + rf)];
+      for (int j = 0; j < 2; ++j) scb[j] = sc[4 * (256 + 128 * j + 32 * wc + rf)] >> sc_sh;
     }
   };
-  const int sc_sh = 8 * (lane >> 5);
 
   using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
   Acc acc[NI][2][NA][NB];  // [A half][B half][row fragment][column fragment]
@@ -276,10 +278,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
         for (int g = 0; g < NB; ++g) {
           const Acc c = (zero && h == 0) ? Acc{} : acc[i][j][f][g];
-          if constexpr (MX)
-            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                bf[g][h], af[f][h], c, 0, 0, 0, (int)(scb[j] >> (16 * h + sc_sh)), 0,
-                (int)(sca[i][f] >> (16 * h + sc_sh)));
+          if constexpr (MX) {
+            if (h == 0)
+              acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                  bf[g][h], af[f][h], c, 0, 0, 0, (int)scb[j], 0, (int)sca[i][f]);
+            else
+              acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                  bf[g][h], af[f][h], c, 0, 0, 2, (int)scb[j], 2, (int)sca[i][f]);
+          }
           else if constexpr (FP8)
             acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
                                                                               0, 0, 0);
