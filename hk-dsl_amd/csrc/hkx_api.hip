@@ -657,7 +657,10 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       d.ep = fused;
       mode = p.pair ? hkx::kDecPair : hkx::kDecOut;
     }
-    if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair)) {
+    if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair) && hkx::rows_takes(d)) {
+      const dim3 g(std::min((a.n + 3) / 4, cu_count()));
+      rc = launched(hkx::launch_rows(d, g, s), "decode GEMM");
+    } else if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair)) {
       const dim3 g(std::min((a.n + 15) / 16, cu_count()));
       rc = launched(hkx::launch_stream(d, g, s), "decode GEMM");
     } else {

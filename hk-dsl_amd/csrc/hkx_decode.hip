@@ -1,5 +1,6 @@
 // Decode GEMM kernels: 4, 8 or 16 waves, 16 or 32 rows of W a workgroup, 1 or 2
-// 16-token fragments, every store mode.
+// 16-token fragments, every store mode; the stream kernel; and the whole-row kernel, defined
+// here (it is launched from this file only).
 #include "hkx_launch.hpp"
 
 namespace hkx {
@@ -85,6 +86,222 @@ static hipError_t launch_stream_ep(const DecodeArgs& a, dim3 grid, hipStream_t s
     case 4: hipLaunchKernelGGL((stream_kernel<4, EPF, MF>), grid, block, 0, s, a); break;
     default: hipLaunchKernelGGL((stream_kernel<0, EPF, MF>), grid, block, 0, s, a); break;
   }
+  return hipGetLastError();
+}
+
+// The whole-row decode GEMM: K = 4096, M <= 4, the fast epilogue form without a tile
+// operand. A chunk is 4 whole rows of W (32 KB, contiguous when W's rows are), and the
+// workgroups take chunks strided by the grid (workgroup g: chunks g, g + G, ...), so at any
+// moment the GPU streams one contiguous window of W. A load-only kernel read W 1.2 us
+// faster (of 16.7) this way than in the stream kernel's chunks of 16 rows x 2 KB, which
+// the 16-row MFMA fragment otherwise needs.
+//
+// The MFMA still takes 16 rows: a chunk's 16 pseudo-rows are (row r, K quarter s), i = 4 r
+// + s, and X enters as 16 columns (token t, quarter s'), 4 t + s', so one
+// v_mfma_f32_16x16x32_bf16 a k-step covers every quarter of 4 rows for 4 tokens, and the
+// products wanted are those with s = s' (a lane's component l % 4 of its D fragment),
+// summed over the quad of lanes 4 t + [0, 4) by two DPP adds. X is the same for every chunk:
+// each wave loads its share (k-steps 4 w .. 4 w + 3 of each quarter) into registers once.
+// Past M = 4 (two or four 4-token blocks of X, an MFMA each a k-step) the form measured
+// slower than the stream kernel (M = 16: 22.8 against 18.6 us at 12288 x 4096): every chunk
+// spans all of K, so a workgroup needs all of X (up to 128 KB) before its first chunk, where
+// the stream kernel spreads it over its first block's chunks (without the X loads: 19.8 us).
+//
+// LDS: a ring of four 32 KB chunk slots (chunk q + 3 in flight while q is multiplied), row r
+// at 8 KB r, its 16-byte piece P holding global piece P ^ (4 r + P / 128) (XOR within the
+// quarter, applied on the global side of the DMA), so the 16 lanes of one k-group reading
+// (r, s) pairs hit 16 different banks. Partial sums: the 8 waves' quad sums of a group of 4
+// chunks, double-buffered by group parity; wave 0 adds them, applies the epilogue and stores
+// after the next group's first barrier, under the other waves' MFMAs.
+__global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
+  constexpr int NW = 8;
+  constexpr int CH = 32768;  // a chunk: 4 rows x 8 KB
+  constexpr int NR = 4;      // ring slots
+  constexpr int GC = 4;      // chunks a group (one reduction and epilogue a group)
+  constexpr int RED = NR * CH;
+  constexpr int EPV = RED + 2 * NW * GC * 64;  // then the bias words: [group % 3][32 B]
+  __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * 32];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nck = (p.N + 3) / 4;
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  if (g >= nck) return;
+  const int nq = (nck - g + G - 1) / G;  // this workgroup's chunks: g + q G
+  auto chunk_of = [&](int q) { return g + q * G; };
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, p.a_bytes);
+
+  // fills: wave w moves half of row w / 2 of a chunk, 1 KB an instruction; the chunk's
+  // offset goes in the per-lane offset, so rows past N read zero through the bound
+  uint32_t fv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wave >> 1, P = (wave & 1) * 256 + i * 64 + lane;
+    fv[i] = (uint32_t)r * p.ldb_b + (uint32_t)((P ^ (4 * r + (P >> 7))) << 4);
+  }
+  // Past the last chunk a fill is still issued, out of range (it reads nothing and writes a
+  // slot no one reads again: chunk q - 4's, done before the barrier that precedes it), so
+  // every wave issues the same loads on every path: the compiler's own waits for X, which
+  // count the loads after X on the path with the fewest, then never drain the ring.
+  auto fill = [&](int q) {
+    const uint32_t base = q < nq ? (uint32_t)chunk_of(q) * 4u * p.ldb_b : 0x80000000u;
+    uint8_t* slot = ring + (q & (NR - 1)) * CH + (wave >> 1) * 8192 + (wave & 1) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf_load16_lds<kNonTemporal>(rw, slot + i * 1024, fv[i] + base, 0);
+  };
+
+  const Fused& e = p.ep;
+  const bool fused = e.form == HKX_EP_FUSED;
+  const bool ra_vec = fused && e.ra.p && e.ra.ld;
+  // broadcast operands read (and their product formed) before any fill is issued: a use
+  // after the fills would wait for every fill in flight (loads complete in order)
+  const float cs_sc = (fused && e.cs.p) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : (fused ? e.cmul : 1.0f);
+  const float rs_sc = (fused && e.rs.p) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
+  const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
+  const float sc = cs_sc * rs_sc;
+  const float add0 = ra_sc + e.cadd;
+  __builtin_amdgcn_sched_barrier(0);
+  // group j's bias words (bf16 of unit stride, 4-byte aligned, N even): chunk c's 4 values
+  // as 2 dwords at 8 c, by 4-byte DMA from 8 lanes of wave 0, a group ahead
+  auto ep_load = [&](int j) {
+    if (wave != 0 || !ra_vec) return;
+    const int q = GC * j + (lane >> 1);
+    const uint32_t off = lane < 8 && q < nq ? (uint32_t)(chunk_of(q) * 8 + 4 * (lane & 1)) : 0x7fffffffu;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(e.ra.p, (uint32_t)p.N * 2u),
+                                             (__attribute__((address_space(3))) void*)(ring + EPV + (j % 3) * 32),
+                                             4, off, 0, 0, 0);
+  };
+  const int nvec = ra_vec ? 1 : 0;
+
+  // X: k-step t of this wave (4 w + t of each quarter): lane l holds token (l % 16) / 4,
+  // quarter l % 4, the 8 values at 8 (l / 16) of the k-step (tokens past M read zero)
+  i32x4 xr[4];
+  {
+    const int tl = (lane & 15) >> 2, sq = lane & 3, kq = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      xr[t] = buf_load16(rx, (uint32_t)tl * p.lda_b + sq * 2048 + (4 * wave + t) * 64 + kq * 16, 0);
+  }
+  // the A fragment's LDS offsets within a slot: lane l reads pseudo-row l % 16 = (r, s),
+  // piece 128 s + 4 k + l / 16 of row r for k-step k
+  uint32_t wa[4];
+  {
+    const int r = (lane & 15) >> 2, sq = lane & 3, kq = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int gp = 128 * sq + 4 * (4 * wave + t) + kq;
+      wa[t] = (uint32_t)(r * 8192 + ((gp ^ (4 * r + sq)) << 4));
+    }
+  }
+  f32x4 acc[GC];
+#pragma unroll
+  for (int c = 0; c < GC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto mma = [&](int q, f32x4& a) {
+    const uint8_t* slot = ring + (q & (NR - 1)) * CH;
+    i32x4 w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t] = *(const i32x4*)(slot + wa[t]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[t]),
+                                                  __builtin_bit_cast(bf16x8, xr[t]), a, 0, 0, 0);
+  };
+  auto red_at = [&](int par, int w2, int c) {
+    return (uint32_t)(RED + (((par * NW + w2) * GC + c) * 64));
+  };
+  // a group's quad sums: lane l's component l % 4 is row l / 16 of the chunk, token
+  // (l % 16) / 4, quarter l % 4; the quad's four quarters summed, one lane of the quad
+  // writes the float at (l / 4) % 16
+  auto group_done = [&](int j) {
+    const int sel = lane & 3;
+#pragma unroll
+    for (int c = 0; c < GC; ++c) {
+        const f32x4 a = acc[c];
+        float x = sel == 0 ? a.x : sel == 1 ? a.y : sel == 2 ? a.z : a.w;
+        x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+        x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+        if (sel == 0) *(float*)(ring + red_at(j & 1, wave, c) + (lane >> 2) * 4) = x;
+        acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // group j's outputs (wave 0): lane l is chunk l / 16 of the group, row (l / 4) % 4 of the
+  // chunk, token l % 4
+  auto finish = [&](int j) {
+    const int c = lane >> 4, r = (lane >> 2) & 3, tl = lane & 3;
+    const int q = GC * j + c;
+    const int n = 4 * chunk_of(q) + r;
+    const bool ok_n = q < nq && n < p.N;
+    float add = add0;
+    if (ra_vec) add = bf16_to_f32(*(const uint16_t*)(ring + EPV + (j % 3) * 32 + 8 * c + 2 * r)) + e.cadd;
+    {
+      float v = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) v += *(const float*)(ring + red_at(j & 1, w2, c) + (lane & 15) * 4);
+      const int m = tl;
+      if (fused) v = act4(e.act, f32x4{v * sc + add, 0.f, 0.f, 0.f}).x;
+      if (ok_n && m < p.M) {
+        const int64_t idx = (int64_t)m * p.ldc + n;
+        if (p.c_dt == HKX_BF16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+        else if (p.c_dt == HKX_FP16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_f16x2(v, 0.f) & 0xffffu);
+        else if (p.c_dt == HKX_FP32) ((float*)p.c)[idx] = v;
+        else if (p.c_dt == HKX_FP8E4M3) ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_e4m3(v);
+        else ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_i8(v);
+      }
+    }
+  };
+  // chunk q landed (with X before it) and every wave is done with chunk q - 1, whose slot
+  // the fill of q + 3 takes: the loads issued after f(q) are f(q + 1) and f(q + 2), 4 a wave
+  // each, and, on wave 0 at the group's second chunk, the bias DMA of the next group;
+  // lgkmcnt(0) as well
+  auto wait_chunk = [&](bool ep_before) {
+    if (ep_before && wave == 0 && nvec) __builtin_amdgcn_s_waitcnt(wait_vm_dec(9) & ~(15 << 8));
+    else __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
+  };
+
+  ep_load(0);
+  __builtin_amdgcn_sched_barrier(0);  // the bias and X before the fills: the waits count in order
+  fill(0);
+  fill(1);
+  fill(2);
+  const int ngr = (nq + GC - 1) / GC;
+  for (int j = 0; j < ngr; ++j) {
+#pragma unroll
+    for (int c = 0; c < GC; ++c) {
+      const int q = GC * j + c;
+      if (q < nq) {
+        wait_chunk(c == 1 && GC * (j + 1) < nq);
+        __builtin_amdgcn_s_barrier();
+        if (c == 0 && GC * (j + 1) < nq) ep_load(j + 1);  // older than the fill of q + 3
+        __builtin_amdgcn_sched_barrier(0);
+        fill(q + 3);
+        if (c == 0 && j > 0 && wave == 0) finish(j - 1);
+        mma(q, acc[c]);
+      }
+    }
+    group_done(j);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last partial sums written
+  __builtin_amdgcn_s_barrier();
+  if (wave == 0) finish(ngr - 1);
+  __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // no fill lands in LDS after the exit
+}
+
+// Whether the whole-row kernel takes a call the stream kernel takes: K = 4096, M <= 4, N up
+// to 32768, the fast epilogue form without a tile operand (every chunk's byte offset then
+// fits 32 bits). At the LM head's N (151936) it measured 1% faster at M = 1 and 3% slower at
+// M = 4 than the stream kernel, whose long runs of blocks reach the same rate there.
+bool rows_takes(const DecodeArgs& a) {
+  const bool tile = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
+  return a.g_total == 32 && a.M <= 4 && a.N <= 32768 && stream_fast(a) && !tile;
+}
+
+hipError_t launch_rows(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL(rows_kernel, grid, dim3(512), 0, s, a);
   return hipGetLastError();
 }
 

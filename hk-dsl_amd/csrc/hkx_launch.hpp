@@ -64,6 +64,9 @@ hipError_t launch_decode(const DecodeArgs& a, int waves, int fn, int mf, int mod
 // no split, unpaired.
 bool stream_takes(const DecodeArgs& a, int splits, bool pair);
 hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s);
+// the whole-row decode kernel (K = 4096, M <= 4, N <= 32768), for calls stream_takes accepts
+bool rows_takes(const DecodeArgs& a);
+hipError_t launch_rows(const DecodeArgs& a, dim3 grid, hipStream_t s);
 
 hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool program, dim3 grid,
                          hipStream_t s);

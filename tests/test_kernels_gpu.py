@@ -396,6 +396,52 @@ def test_decode_stream(m, nk):
     assert (c[:, n:].float() == 7.0).all()
 
 
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 8, 9, 13, 16])
+@pytest.mark.parametrize("n", [12288, 1004, 4100, 8])
+def test_decode_rows(m, n):
+    """The whole-row decode kernel at M <= 4 (K = 4096: chunks of 4 rows strided over the
+    workgroups), the stream kernel above: bias, chunk counts a workgroup from 1 up (1025
+    chunks: one workgroup with a group of one), a W of row stride K + 64, an output of row
+    stride N + 8 with sentinels (columns past N never written)."""
+    k = 4096
+    a, b = _data(m, n, k, seed=31)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias", O.gemm_fp32(a, b), bias=bias)
+    wide = torch.zeros(n, k + 64, dtype=b.dtype)
+    wide[:, :k] = b
+    c = torch.full((m, n + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+    bd = bias.to(DEV)
+    _run(a.to(DEV), wide.to(DEV)[:, :k], c[:, :n], kernel=nat.KERNEL_DECODE,
+         variant=nat.DEC_STREAM, ep=_fused([(bd, nat.ROW)], ra=0))
+    O.assert_close(c[:, :n], ref, rtol=1e-2, atol=1e-2)
+    assert (c[:, n:].float() == 7.0).all()
+
+
+@pytest.mark.parametrize("m", [1, 3, 7, 16])
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "fp16", "fp32"])
+def test_decode_rows_forms(m, odt):
+    """The decode kernels' epilogue forms and output types (the whole-row kernel at M = 1 and
+    3, the stream kernel at 7 and 16): none, and a broadcast per-token scale with cmul, a bias,
+    cadd and GELU."""
+    n, k = 1000, 4096
+    a, b = _data(m, n, k, seed=33)
+    acc = O.gemm_fp32(a, b)
+    ad, bdev = a.to(DEV), b.to(DEV)
+    c = torch.empty((m, n), dtype=odt, device=DEV)
+    _run(ad, bdev, c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM)
+    O.assert_close(c, acc, rtol=1e-2, atol=1e-2)
+    g = torch.Generator().manual_seed(34)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    sd = torch.full((1, 1), 0.75, device=DEV).expand(m, 1)
+    bd = bias.to(DEV)
+    ep = _fused([(sd, nat.COL), (bd, nat.ROW)], cs=0, ra=1, act=nat.ACT_GELU_TANH,
+                cmul=0.5, cadd=0.25)
+    c2 = torch.empty((m, n), dtype=odt, device=DEV)
+    _run(ad, bdev, c2, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM, ep=ep)
+    O.assert_close(c2, O.gelu_tanh(acc * 0.375 + bias.float() + 0.25), rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("m", [1, 7, 16, 20, 32])
 @pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024), (1000, 6144)])
 def test_decode_stream_fused_forms(m, nk):
