@@ -442,6 +442,30 @@ def test_decode_rows_forms(m, odt):
     O.assert_close(c2, O.gelu_tanh(acc * 0.375 + bias.float() + 0.25), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("m", [1, 4])
+def test_decode_rows_quantizing_stores(m):
+    """The whole-row decode kernel's 8-bit stores, one byte a lane: int8 and fp8 e4m3
+    (saturating at 448) of acc times a broadcast per-token scale."""
+    n, k = 4096, 4096
+    a, b = _data(m, n, k, seed=35)
+    acc = O.gemm_fp32(a, b)
+    ad, bdev = a.to(DEV), b.to(DEV)
+    s40 = torch.full((1, 1), 40.0, device=DEV).expand(m, 1)
+    c = torch.empty((m, n), dtype=torch.int8, device=DEV)
+    _run(ad, bdev, c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+         ep=_fused([(s40, nat.COL)], cs=0))
+    assert (c.cpu().float() - O.quantize_int8(acc * 40)).abs().max().item() <= 1.0
+    s300 = torch.full((1, 1), 300.0, device=DEV).expand(m, 1)
+    c8 = torch.empty((m, n), dtype=torch.float8_e4m3fn, device=DEV)
+    _run(ad, bdev, c8, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+         ep=_fused([(s300, nat.COL)], cs=0))
+    want = (acc * 300).clamp(-448, 448)
+    got = c8.cpu().float()
+    big = want.abs() > 16
+    assert ((got - want).abs() / want.abs())[big].max().item() < 0.07
+    assert got.abs().max().item() == 448.0
+
+
 @pytest.mark.parametrize("m", [1, 7, 16, 20, 32])
 @pytest.mark.parametrize("nk", [(1000, 2048), (12288, 1024), (1000, 6144)])
 def test_decode_stream_fused_forms(m, nk):
