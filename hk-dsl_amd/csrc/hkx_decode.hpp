@@ -255,16 +255,27 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
     const int r = 2 * wave + (i >> 1), h = i & 1;
     fv[i] = (uint32_t)r * p.ldb_b + (uint32_t)(((64 * h + lane) ^ r) << 4);
   }
+  // With X streamed (CPB = 0) a fill past the last chunk is still issued, out of range (it
+  // reads nothing and writes a slot no one reads again: chunk q - 4's, done before the
+  // barrier that precedes it), so every wave issues the same loads on every path: the
+  // compiler's own waits for X count the loads after X on the path with the fewest, and with
+  // fills skipped at the end they had drained the ring before every chunk's MFMAs (1.1-1.6
+  // us of 19.7-24 at the down projections' K). With X held (loaded in the first block only)
+  // such a drain comes once a launch; there the fills stop at the end (issuing them
+  // measured up to 0.5 us slower at M = 16).
+  constexpr bool kAllFills = CPB == 0;
   auto fill = [&](int q) {
-    if (q >= nq) return;  // past the end: nothing (the waits count what was issued)
-    const int jb = q / cpb, kc = kchunk(q - jb * cpb);
+    if (!kAllFills && q >= nq) return;  // past the end: nothing (the waits count what was issued)
+    const bool live = q < nq;
+    const int jb = live ? q / cpb : 0, kc = live ? kchunk(q - jb * cpb) : 0;
     const int bi = block_of(jb);
-    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u);
+    const uint32_t so = live ? __builtin_amdgcn_readfirstlane((uint32_t)bi * 16u * p.ldb_b + (uint32_t)kc * 2048u) : 0u;
+    const uint32_t oob = live ? 0u : 0x80000000u;
     uint8_t* slot = ring + (q & (NR - 1)) * CH;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 2 * wave + (i >> 1), h = i & 1;
-      buf_load16_lds<kNonTemporal>(rw, slot + r * 2048 + h * 1024, fv[i], so);
+      buf_load16_lds<kNonTemporal>(rw, slot + r * 2048 + h * 1024, fv[i] + oob, so);
     }
   };
   // The epilogue's vector operands of block j (row scale per token m, column scale and
@@ -415,19 +426,21 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   };
 
   // X for chunk k (its group of this wave) goes to registers by loads issued just before
-  // the fill of chunk k + 1: x0 f0 x1 f1 f2, then step q issues x(q + 2) and f(q + 3). X for
-  // a chunk exists for every chunk with CPB = 0 (streamed), for the first CPB with CPB > 0
-  // (held across the walk).
-  auto has_x = [&](int k) { return k < nq && (CPB == 0 || k < CPB); };
+  // the fill of chunk k + 1: x0 f0 x1 f1 f2, then step q issues x(q + 2) and f(q + 3). X is
+  // loaded for every step with CPB = 0 (streamed; past the last chunk too, like the fills,
+  // into a register slot no one reads), for the first CPB chunks with CPB > 0 (held across
+  // the walk; a workgroup has at least CPB chunks).
+  auto has_x = [&](int k) { return CPB == 0 || k < CPB; };
   // chunk q and its X landed, and every wave is done with chunk q - 1, whose slot the fill
   // of q + 3 takes: in issue order the loads after x(q) and f(q) are f(q + 1), x(q + 1) and
-  // f(q + 2), each 4 a wave where it exists (anything issued later only makes the wait
+  // f(q + 2), 4 a wave each where they are issued (anything issued later only makes the wait
   // stricter); lgkmcnt(0) as well
   // wave 0's epilogue-vector DMAs of the step before (ep_load) are among them too
   const int nvec = EPF == kStreamEpFast ? (int)ra_vec + ta_n
                                         : (int)cs_vec + (int)rs_vec + (int)ra_vec + ta_n;
   auto wait_chunk = [&](int q, bool ep_before) {
-    const int n = 4 * ((q + 1 < nq) + (q + 2 < nq)) + 4 * MF * has_x(q + 1) + (ep_before && wave == 0 ? nvec : 0);
+    const int n = (kAllFills ? 8 : 4 * ((q + 1 < nq) + (q + 2 < nq))) + 4 * MF * has_x(q + 1) +
+                  (ep_before && wave == 0 ? nvec : 0);
     switch (n) {
 #define HKX_WAIT_CASE(N) case N: __builtin_amdgcn_s_waitcnt(wait_vm_dec(N) & ~(15 << 8)); break;
       HKX_WAIT_CASE(1) HKX_WAIT_CASE(2) HKX_WAIT_CASE(3) HKX_WAIT_CASE(4) HKX_WAIT_CASE(5)
