@@ -193,9 +193,11 @@ typedef struct HkxEpilogue {
                                  (gemm_cdna.py:57-586). Combines with the two bits above */
 
 /* HKX_KERNEL_DECODE variant bits. */
-#define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W blocks (M <= 16, K a multiple
-                             of 1024 up to 32768, no split, unpaired); other calls take the
-                             blocked kernel */
+#define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W (M <= 16, or M <= 32 from K =
+                             2048; K a multiple of 1024 up to 32768, no split, unpaired): in
+                             blocks of 16 rows, or, at K = 4096, M <= 4, N <= 32768 with no
+                             residual and no vector scale, in chunks of 4 whole rows strided
+                             over the workgroups; other calls take the blocked kernel */
 
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */
