@@ -262,8 +262,8 @@ __global__ void __launch_bounds__(512) stream_kernel(const DecodeArgs p) {
   // fills skipped at the end they had drained the ring before every chunk's MFMAs (1.1-1.6
   // us of 19.7-24 at the down projections' K). With X held (loaded in the first block only)
   // such a drain comes once a launch; there the fills stop at the end (issuing them
-  // measured 0.2-0.6 us slower at M = 8-16 on 12288 and 28672 rows of W, 0.6 faster only at
-  // 6144 rows and M = 16, in interleaved same-box runs).
+  // measured 0.2-0.6 us slower at M = 8-16 on 12288 and 28672 rows of W and 0.4-0.7 us
+  // slower on 1536 and 4096 rows, in interleaved same-box runs).
   constexpr bool kAllFills = CPB == 0;
   auto fill = [&](int q) {
     if (!kAllFills && q >= nq) return;  // past the end: nothing (the waits count what was issued)
