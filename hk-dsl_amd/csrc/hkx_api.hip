@@ -220,6 +220,9 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   int kernel = a->kernel, bm = a->tile_m, bn = a->tile_n, splits = a->splits;
   if (kernel == HKX_KERNEL_AUTO) auto_choose(a, &kernel, &bm, &bn, &splits);
   if (splits < 1) splits = 1;
+  if (e5m2_pair(a->ab_dtype) && pair)
+    return fail(HKX_ERR_ARG, "the paired silu-and-mul epilogue is not built for e5m2 operands "
+                "(bf16 and fp8-e4m3 only)");
   if (e5m2_pair(a->ab_dtype) &&
       (kernel != HKX_KERNEL_TILE || bm != 256 || bn != 256 ||
        (a->tile_schedule != HKX_TILE_RING && a->tile_schedule != HKX_TILE_AUTO) || a->variant))

@@ -119,8 +119,12 @@ __global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
   constexpr int NR = 4;      // ring slots
   constexpr int GC = 4;      // chunks a group (one reduction and epilogue a group)
   constexpr int RED = NR * CH;
-  constexpr int EPV = RED + 2 * NW * GC * 64;  // then the bias words: [group % 3][32 B]
-  __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * 32];
+  // then the bias words, three slots by group: [group % 3][256 B]. A slot is 256 bytes, not
+  // the 32 its 8 values take, because the DMA runs on all 64 lanes of wave 0 and each lane,
+  // in range or not, writes its dword at 4 * lane
+  constexpr int EPV = RED + 2 * NW * GC * 64;
+  constexpr int EPS = 256;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[EPV + 3 * EPS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -172,7 +176,7 @@ __global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
     const int q = GC * j + (lane >> 1);
     const uint32_t off = lane < 8 && q < nq ? (uint32_t)(chunk_of(q) * 8 + 4 * (lane & 1)) : 0x7fffffffu;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(e.ra.p, (uint32_t)p.N * 2u),
-                                             (__attribute__((address_space(3))) void*)(ring + EPV + (j % 3) * 32),
+                                             (__attribute__((address_space(3))) void*)(ring + EPV + (j % 3) * EPS),
                                              4, off, 0, 0, 0);
   };
   const int nvec = ra_vec ? 1 : 0;
@@ -237,7 +241,7 @@ __global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
     const int n = 4 * chunk_of(q) + r;
     const bool ok_n = q < nq && n < p.N;
     float add = add0;
-    if (ra_vec) add = bf16_to_f32(*(const uint16_t*)(ring + EPV + (j % 3) * 32 + 8 * c + 2 * r)) + e.cadd;
+    if (ra_vec) add = bf16_to_f32(*(const uint16_t*)(ring + EPV + (j % 3) * EPS + 8 * c + 2 * r)) + e.cadd;
     {
       float v = 0.f;
 #pragma unroll

@@ -231,7 +231,7 @@ def linear(x, weight, bias=None):
     k = x.shape[-1]
     n = weight.shape[0]
     m = x.numel() // k if k else 0
-    key = (m, n, k, x.dtype, weight.dtype, None if bias is None else bias.dtype,
+    key = (m, n, k, x.dtype, weight.dtype, None if bias is None else (bias.dtype, tuple(bias.shape)),
            _weight_ok(weight), x.get_device())
     plan = ROUTER.plans.get(key)
     if plan is None:

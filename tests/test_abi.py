@@ -80,6 +80,12 @@ def test_argument_checks():
     # fp8 takes K in 128s
     rc, msg = _check(_args(ab_dtype=nat.FP8E4M3, k=192, lda=192, ldb=192))
     assert rc == nat.ERR_SHAPE and "multiple of 128" in msg
+    # the paired silu-and-mul form is bf16 / e4m3 only: an e5m2 pair is refused for that
+    e5 = _args(ab_dtype=nat.FP8E5M2, k=256, lda=256, ldb=256, m=256, n=256, tile_m=256,
+               tile_n=256, kernel=nat.KERNEL_TILE)
+    e5.ep.form = nat.EP_SILU_MUL
+    rc, msg = _check(e5)
+    assert rc == nat.ERR_ARG and "silu-and-mul" in msg and "e5m2" in msg
 
 
 def test_epilogue_checks():

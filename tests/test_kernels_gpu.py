@@ -417,6 +417,24 @@ def test_decode_rows(m, n):
     assert (c[:, n:].float() == 7.0).all()
 
 
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("n", [16384, 20004, 32768])
+def test_decode_rows_bias_many_groups(m, n):
+    """The whole-row decode kernel with a bias where a workgroup walks 4 or more groups of
+    chunks (N > 12288 on 256 CUs), so the three bias slots of its LDS are each reused: a
+    DMA of one group's bias words must leave the other slots' words alone (N = 20004 also
+    ends on a ragged chunk)."""
+    k = 4096
+    a, b = _data(m, n, k, seed=36)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(37)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias", O.gemm_fp32(a, b), bias=bias)
+    c = torch.full((m, n + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), b.to(DEV), c[:, :n], kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM,
+         ep=_fused([(bias.to(DEV), nat.ROW)], ra=0))
+    O.assert_close(c[:, :n], ref, rtol=1e-2, atol=1e-2)
+    assert (c[:, n:].float() == 7.0).all()
+
+
 @pytest.mark.parametrize("m", [1, 3, 7, 16])
 @pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16, torch.float32],
                          ids=["bf16", "fp16", "fp32"])
