@@ -9,6 +9,8 @@ namespace {
 
 bool vec16_16(const Opnd& o) { return o.p && o.dt == HKX_BF16 && o.ld == 1 && ((uintptr_t)o.p & 15) == 0; }
 bool vec32_16(const Opnd& o) { return o.p && o.dt == HKX_FP32 && o.ld == 1 && ((uintptr_t)o.p & 15) == 0; }
+// an fp32 scale of one value (stride 0), read once by the kernel
+bool one32(const Opnd& o) { return o.p && o.dt == HKX_FP32 && o.ld == 0 && ((uintptr_t)o.p & 3) == 0; }
 
 // The compiled epilogue form the quadrant kernel runs a call with, or -1 if it does not
 // take the call. Vector operands reach LDS by 16-byte DMA: unit stride, 16-byte aligned.
@@ -31,7 +33,7 @@ int quad_form(const TileArgs& a, bool fp8, int mode) {
   if (fp8) {
     if (e.act != HKX_ACT_NONE) return -1;
     if (!e.cs.p && !e.rs.p && !e.ra.p) return kEpNone;
-    if (!vec32_16(e.cs) || !vec32_16(e.rs)) return -1;
+    if (!(vec32_16(e.cs) || one32(e.cs)) || !(vec32_16(e.rs) || one32(e.rs))) return -1;
     if (!e.ra.p) return kEpDeq;
     return vec16_16(e.ra) ? kEpDeqBias : -1;
   }

@@ -190,8 +190,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       wave == 0 ? (deq ? e.cs.p : nullptr) : wave == 1 ? (deq ? e.rs.p : nullptr) : (bias ? e.ra.p : nullptr),
       wave == 0 ? (deq ? (uint32_t)p.M * 4u : 0u)
                 : wave == 1 ? (deq ? (uint32_t)p.N * 4u : 0u) : (bias && e.ra.p ? (uint32_t)p.N * 2u : 0u));
+  // a scale of one value (stride 0) is read once here, before any fill (a read after the
+  // fills would wait for all of them), and has no DMA
+  const bool cs_bc = deq && e.cs.ld == 0, rs_bc = deq && e.rs.ld == 0;
+  [[maybe_unused]] const float cs0 = cs_bc ? ld1(e.cs.p, HKX_FP32, 0) : 1.0f;
+  [[maybe_unused]] const float rs0 = rs_bc ? ld1(e.rs.p, HKX_FP32, 0) : 1.0f;
   auto vec_load = [&](int lt) {
     if (wave > 2 || (wave < 2 && !deq) || (wave == 2 && !bias)) return;
+    if ((wave == 0 && cs_bc) || (wave == 1 && rs_bc)) return;
     int m0, n0;
     tile_at(lt, m0, n0);
     const uint32_t so = wave == 0 ? (uint32_t)m0 * 4u : wave == 1 ? (uint32_t)n0 * 4u : (uint32_t)n0 * 2u;
@@ -354,7 +360,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int f = 0; f < 2; ++f) cs[i][f] = ((const float*)ev)[128 * i + 64 * grp + 32 * f + rf];
+          for (int f = 0; f < 2; ++f) cs[i][f] = cs_bc ? cs0 : ((const float*)ev)[128 * i + 64 * grp + 32 * f + rf];
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -366,7 +372,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int col = cb + 16 * t + 8 * u + 4 * h;
-            if constexpr (deq) rs[t][u] = *(const f32x4*)(ev + 1024 + col * 4);
+            if constexpr (deq) rs[t][u] = rs_bc ? f32x4{rs0, rs0, rs0, rs0} : *(const f32x4*)(ev + 1024 + col * 4);
             if constexpr (bias) bv[t][u] = unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
           }
         // after the 16-lane trade below, lane l stores row 16 s + l % 16 of the fragment

@@ -87,3 +87,28 @@ def test_mid_m_splits_over_k(m, n, k, route):
     a8, b8, sa, sb, bias = _ops(m, n, k, E4, E4, seed=m + k)
     got = hk.ops.scaled_mm(a8.to(DEV), b8.to(DEV), sa.to(DEV), sb.to(DEV), bias=bias.to(DEV))
     O.assert_close(got, O.scaled_mm(a8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("form", ["one_one", "one_vec", "vec_one", "tensor_one"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_e4m3_one_value_scales_on_the_256_tiles(form, with_bias):
+    """Per-tensor scales (one value, stride 0) on the 256 x 256 tile kernels, mixed with
+    per-row / per-channel ones: the quadrant kernel reads a one-value scale once and DMAs
+    only the vector ones. Ragged M and N (520 x 776), two tiles a column."""
+    m, n, k = 520, 776, 1024
+    a8, b8, sa, sb, bias = _ops(m, n, k, E4, E4, seed=16)
+    sa_d, sb_d = sa.to(DEV), sb.to(DEV)
+    if form == "one_one":
+        sa_x, sb_x, sa_r, sb_r = 0.03, 0.02, 0.03, 0.02
+    elif form == "one_vec":
+        sa_x, sb_x, sa_r, sb_r = 0.03, sb_d, 0.03, sb
+    elif form == "vec_one":
+        sa_x, sb_x, sa_r, sb_r = sa_d, 0.02, sa, 0.02
+    else:  # 0-d device tensors
+        sa_x, sb_x = torch.tensor(0.03, device=DEV), torch.tensor(0.02, device=DEV)
+        sa_r, sb_r = 0.03, 0.02
+    bb = bias.to(DEV) if with_bias else None
+    got = hk.ops.scaled_mm(a8.to(DEV), b8.to(DEV), sa_x, sb_x, bias=bb, schedule="t256")
+    ref = O.scaled_mm(a8, b8, sa_r, sb_r, bias if with_bias else None)
+    O.assert_close(got, ref, rtol=3e-2, atol=1e-2)
+    assert O.rel_to_max(got.cpu(), ref) < 8e-3
