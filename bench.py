@@ -122,28 +122,83 @@ def _inputs(m, k, n, seed, dev):
     return x.to(dev), w.t().contiguous().to(dev), b.to(dev)
 
 
+def _cpu_median(fn, runs=5):
+    fn()  # warm-up
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 def cpu_baseline(x, wt, b):
-    """The oracle on the host: torch fp32 y = gelu_tanh(x @ w + b) at config 2's full size,
-    median of 3 timed runs after a warm-up (all host threads)."""
+    """The oracle on the host (torch fp32 closed forms, all host threads), each BASELINE
+    config on the same seeded inputs as its GPU arm, the median of 5 timed runs after a
+    warm-up. The top-level figure is config 2's, the bench's workload; "configs" holds
+    each config's own. Config 3 at M = 8192 runs on a bounded row sample (1024 rows of x:
+    a GEMM's rate is flat in M at these sizes), named in its "sample"."""
     import torch
 
     from oracle import gemm_oracle as O
 
     torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
     xc, wc, bc = x.cpu().float(), wt.cpu().float().t().contiguous(), b.cpu().float()
-    O.linear_bias_gelu(xc[:256], wc, bc)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.linear_bias_gelu(xc, wc, bc)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
     m, k = xc.shape
     n = wc.shape[1]
-    return {"value": round(2 * m * n * k / t / 1e12, 3), "unit": "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+    t2 = _cpu_median(lambda: O.linear_bias_gelu(xc, wc, bc))
+    cfgs = {}
+
+    def put(name, flops, t, sample, byts=None):
+        r = {"TFLOP/s": round(flops / t / 1e12, 4), "s_per_run": round(t, 5), "sample": sample}
+        if byts is not None:
+            r["GB/s"] = round(byts / t / 1e9, 2)
+        cfgs[name] = r
+
+    put("cfg2_bias_gelu", 2.0 * m * n * k, t2, f"full {m}x{k}x{n}")
+    # config 1: linear_bias_gelu 256 x 1024 x 1024
+    x1, w1, b1 = (t.cpu().float() for t in _inputs(256, 1024, 1024, 1, "cpu"))
+    w1 = w1.t().contiguous()
+    put("cfg1_bias_gelu", 2.0 * 256 * 1024 * 1024,
+        _cpu_median(lambda: O.linear_bias_gelu(x1, w1, b1)), "full 256x1024x1024")
+    # config 3: gate_up + silu_and_mul, w (4096, 24576)
+    x3, w3, _ = (t.cpu().float() for t in _inputs(2048, 4096, 24576, 3, "cpu"))
+    w3 = w3.t().contiguous()
+
+    def c3(xs):
+        h = xs @ w3
+        return O.silu_and_mul(h[:, :12288], h[:, 12288:])
+    put("cfg3_gate_up_silu_mul_M2048", 2.0 * 2048 * 24576 * 4096, _cpu_median(lambda: c3(x3)),
+        "full M=2048")
+    put("cfg3_gate_up_silu_mul_M8192", 2.0 * 1024 * 24576 * 4096, _cpu_median(lambda: c3(x3[:1024])),
+        "1024 of the 8192 rows (the rate of the full call, flops counted for the rows run)")
+    del x3, w3
+    # config 4: decode y = x @ W^T (+ bias), W (12288, 4096)
+    w4 = _inputs(1, 4096, 12288, 40, "cpu")[1].float()
+    b4 = _inputs(1, 4096, 12288, 4, "cpu")[2].float()
+    for m4 in (1, 4, 16):
+        x4 = _inputs(m4, 4096, 12288, 4, "cpu")[0].float()
+        byts = 12288 * 4096 * 2 + m4 * 4096 * 2 + m4 * 12288 * 2
+        put(f"cfg4_decode_M{m4}_bias", 2.0 * m4 * 12288 * 4096,
+            _cpu_median(lambda: O.apply_epilogue("bias", O.gemm_fp32(x4, w4), bias=b4)),
+            f"full M={m4} (GB/s counts W, x and y at bf16 size, as the GPU arm)", byts)
+    del w4
+    # config 5: fp8 scaled + dequant + bias, 8192 x 4096 x 4096 (fp8 values exact in fp32)
+    g = torch.Generator().manual_seed(5)
+    x5 = torch.randn(8192, 4096, generator=g).to(torch.float8_e4m3fn)
+    w5 = torch.randn(4096, 4096, generator=g).to(torch.float8_e4m3fn).t().contiguous()
+    sa = (torch.rand(8192, 1, generator=g) * 1.5 + 0.5) / 448
+    sb = (torch.rand(4096, generator=g) * 1.5 + 0.5) / 448
+    bias = (torch.randn(4096, generator=g) * 0.1).to(torch.bfloat16)
+    put("cfg5_fp8_scaled_dequant_bias", 2.0 * 8192 * 4096 * 4096,
+        _cpu_median(lambda: O.scaled_mm(x5, w5, sa, sb, bias)), "full 8192x4096x4096")
+    return {"value": round(2 * m * n * k / t2 / 1e12, 3), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
             "sample": f"oracle linear_bias_gelu at the full config-2 size {m}x{k}x{n} (fp32), "
-                      f"median of 3 runs, {t:.2f} s each"}
+                      f"median of 5 runs after a warm-up, {t2:.2f} s each; "
+                      f"torch.get_num_threads() = {threads}, os.cpu_count() = {os.cpu_count()}",
+            "configs": cfgs}
 
 
 #: The reference's published device times of hk.templates.gemm on MI355X, µs: (layer,
@@ -351,12 +406,18 @@ def main():
     }
     # HBM bytes a launch of this kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     # runs summarised under profiles/ (null if they were taken on another kernel)
+    # (FETCH_SIZE + WRITE_SIZE: the L2's misses, of which the 256 MB Infinity Cache serves
+    # part, so an upper bound on HBM bytes; taken in the profiled runs named in that file)
     tr = os.path.join(ROOT, "profiles", "traffic_quad_bias_gelu_cfg2.json")
     if os.path.isfile(tr):
         with open(tr) as f:
             rec = json.load(f)
         if rec.get("kernel") == kname:
-            res["roofline"]["traffic"] = rec.get("hbm_bytes_per_launch")
+            res["roofline"]["traffic"] = rec.get("l2_miss_bytes_per_launch")
+            res["roofline"]["traffic_source"] = (
+                "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (L2-miss bytes, scaled by a 1 GiB "
+                "copy; an upper bound on HBM bytes: the Infinity Cache serves part of them), "
+                "from the runs in profiles/traffic_quad_bias_gelu_cfg2.json")
     res["measured_peaks"] = peaks
     if not args.quick:
         res["also"] = other_configs(args.steps, args.warmup, peaks)
@@ -377,18 +438,21 @@ def main():
 
 def measured_peaks():
     """This GPU's own ceilings, measured in this run with the build's probe (hk.peaks):
-    the dense MFMA rate of a register-only loop (bf16, fp8) and the HBM read rate of one
-    pass over 2 GiB (past the 256 MB Infinity Cache). Each is the best of 5 launches."""
+    the dense MFMA rate of a register-only loop (bf16, fp8) and the HBM read rate over four
+    1 GiB buffers read in rotation (past the 256 MB Infinity Cache). Each is the best of 5."""
     from hk import peaks
 
+    hbm, hbm_by = peaks.hbm_read_gbs(detail=True)
     return {"mfma_bf16_tflops": round(peaks.mfma_tflops(False), 1),
             "mfma_fp8_tflops": round(peaks.mfma_tflops(True), 1),
             "mfma_bf16_random_operands_tflops": round(peaks.mfma_random_tflops(False), 1),
             "mfma_fp8_random_operands_tflops": round(peaks.mfma_random_tflops(True), 1),
-            "hbm_read_gbs": round(peaks.hbm_read_gbs(), 1),
+            "hbm_read_gbs": round(hbm, 1),
+            "hbm_read_gbs_by_kernel": {k: round(v, 1) for k, v in hbm_by.items()},
             "how": "hk.peaks: register-only 32x32 MFMA loop on every CU, on constant operands "
                    "and on random ones (the power-limited rate on data that toggles like real "
-                   "tensors); one pass of 16-byte non-temporal reads over 2 GiB"}
+                   "tensors); HBM: four 1 GiB buffers read in rotation past the 256 MB "
+                   "Infinity Cache, the best of three read kernels"}
 
 
 def other_configs(steps, warmup, peaks):
@@ -400,6 +464,20 @@ def other_configs(steps, warmup, peaks):
     T = hk.templates.gemm
     dev = "cuda:0"
     out = {}
+    # config 2 on the same box: the plain GEMM (no epilogue) on the same kernel, and
+    # hipBLASLt's plain GEMM (torch.matmul) on the same operands -- what the bias + GELU
+    # epilogue costs, and where the vendor library stands
+    x, wt, b = _inputs(4096, 4096, 12288, 0, dev)
+    y = torch.empty(4096, 12288, device=dev, dtype=torch.bfloat16)
+    fl = 2.0 * 4096 * 12288 * 4096
+    cmp = {}
+    for name, fn in (("quad_plain", lambda: T(x, wt, out=y)),
+                     ("quad_bias_gelu", lambda: T(x, wt, epilogue=T.bias_gelu, bias=b, out=y)),
+                     ("hipblaslt_plain_torch_matmul", lambda: torch.matmul(x, wt.t(), out=y))):
+        t, _, _ = _events_time(fn, steps, warmup)
+        cmp[name] = {"us": round(t * 1e6, 2), "TFLOP/s": round(fl / t / 1e12, 1)}
+    out["cfg2_same_box"] = cmp
+    del x, wt, b, y
     # config 3: fused gate_up + silu_and_mul
     for m in (2048, 8192):
         x, wt, _ = _inputs(m, 4096, 24576, 3, dev)
@@ -449,6 +527,15 @@ def other_configs(steps, warmup, peaks):
                                            "frac_measured_random_operands": round(
                                                fl / t / 1e12 / peaks["mfma_fp8_random_operands_tflops"], 4),
                                            "us": round(t * 1e6, 1)}
+    # the vendor path on the same operands: torch._scaled_mm (hipBLASLt), which takes the
+    # scales but not the bias in this form
+    try:
+        wcol = w8.t()  # (K, N) column-major, as _scaled_mm wants its second operand
+        t, _, _ = _events_time(lambda: torch._scaled_mm(x8, wcol, scale_a=sa, scale_b=sb.reshape(1, -1),
+                                                         out_dtype=torch.bfloat16), steps, warmup)
+        out["cfg5_fp8_scaled_dequant_bias"]["torch_scaled_mm_no_bias_us"] = round(t * 1e6, 1)
+    except Exception as ex:  # noqa: BLE001 - a vendor-side refusal is reported, not fatal
+        out["cfg5_fp8_scaled_dequant_bias"]["torch_scaled_mm_no_bias_us"] = f"unavailable: {str(ex)[:120]}"
     return out
 
 

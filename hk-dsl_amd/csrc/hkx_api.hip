@@ -66,6 +66,10 @@ struct Plan {
   // HKX_RING_STREAMK: columns [0, sk_cut) in whole waves of ring tiles, the rest of N on
   // ring tiles split sk_splits ways over K (sk_kper units each) into the workspace
   int sk_cut, sk_splits, sk_kper;
+  // DECODE split over K, unpaired, not a program: the counters it can finish with (one a
+  // block of rows), and whether this call does (counters given)
+  int ncnt;
+  bool arrive;
 };
 
 int cu_count();
@@ -320,6 +324,17 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
       }
     }
   }
+  p->ncnt = 0;
+  p->arrive = false;
+  if (kernel == HKX_KERNEL_DECODE && p->splits > 1 && !pair && !program) {
+    p->ncnt = (a->n + 16 * p->fn - 1) / (16 * p->fn);
+    if (a->counters) {
+      if (a->counters_len < p->ncnt || !aligned(a->counters, 4))
+        return fail(HKX_ERR_WORKSPACE, "this plan needs %d 4-byte aligned arrival counters "
+                    "(counters_len %lld)", p->ncnt, (long long)a->counters_len);
+      p->arrive = true;
+    }
+  }
   if (ws && (!a->ws || a->ws_bytes < p->ws_bytes || !aligned(a->ws, 16)))
     return fail(HKX_ERR_WORKSPACE, "this plan needs a 16-byte aligned fp32 workspace of %zu bytes",
                 p->ws_bytes);
@@ -491,6 +506,18 @@ size_t hkx_gemm_workspace(const HkxGemmArgs* args) {
   return p.ws_bytes;
 }
 
+size_t hkx_gemm_counters(const HkxGemmArgs* args) {
+  Plan p{};
+  if (!args) return 0;
+  HkxGemmArgs a = *args;
+  a.ws = (void*)(uintptr_t)256;
+  a.ws_bytes = (size_t)-1;
+  a.counters = nullptr;
+  a.counters_len = 0;
+  if (make_plan(&a, &p) != HKX_OK) return 0;
+  return (size_t)p.ncnt;
+}
+
 int hkx_gemm_check(const HkxGemmArgs* args) {
   Plan p{};
   g_err.clear();
@@ -647,7 +674,15 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
     const int outw = p.pair ? 8 * p.fn : 16 * p.fn;
     const dim3 grid((a.n + outw - 1) / outw, p.splits);
     int mode;
-    if (p.via_ws) {
+    if (p.arrive) {  // shares in ws; the last split of a block finishes it into C
+      d.c = a.c;
+      d.ldc = a.ldc;
+      d.ep = fused;
+      d.ws = (float*)a.ws;
+      d.split_stride = (int64_t)a.m * a.n;
+      d.cnt = a.counters;
+      mode = hkx::kDecArrive;
+    } else if (p.via_ws) {
       d.c = a.ws;
       d.ldc = p.pair ? a.n * 2LL : a.n;
       d.split_stride = (int64_t)a.m * wcols;
@@ -672,7 +707,7 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
     if (rc) return rc;
   }
 
-  if (p.via_ws) {
+  if (p.via_ws && !p.arrive) {
     hkx::ReduceArgs r{};
     r.ws = (const float*)a.ws;
     r.split_stride = (int64_t)a.m * wcols;
@@ -698,6 +733,8 @@ int hkx_gemm_noalloc(const HkxGemmArgs* args, void* stream) {
   HkxGemmArgs a = *args;
   a.ws = nullptr;
   a.ws_bytes = 0;
+  a.counters = nullptr;  // a K split is summed by its second launch, from the scratch
+  a.counters_len = 0;
   const size_t need = hkx_gemm_workspace(&a);
   if (need > (size_t)HKX_NOALLOC_SCRATCH_BYTES)
     return fail(HKX_ERR_WORKSPACE,

@@ -20,6 +20,7 @@ static hipError_t launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_
   switch (mode) {
     case kDecOut: hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecOut>), grid, block, 0, s, a); break;
     case kDecWs: hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecWs>), grid, block, 0, s, a); break;
+    case kDecArrive: hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecArrive>), grid, block, 0, s, a); break;
     case kDecPair:
       if constexpr (FN % 2 == 0) { hipLaunchKernelGGL((decode_kernel<NW, FN, MF, U, kDecPair>), grid, block, 0, s, a); break; }
       return hipErrorInvalidValue;

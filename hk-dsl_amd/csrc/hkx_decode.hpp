@@ -34,6 +34,9 @@ struct DecodeArgs {
   int32_t pair_off;
   int32_t c_dt;
   Fused ep;
+  // kDecArrive: the shares' buffer (c is C) and one arrival counter a block of rows
+  float* ws;
+  int32_t* cnt;
 };
 
 // s_waitcnt vmcnt(n) (gfx9 encoding: bits 3:0 and 15:14; expcnt and lgkmcnt left alone)
@@ -43,6 +46,7 @@ constexpr int kDecOut = 0;     // C with the fused epilogue
 constexpr int kDecWs = 1;      // fp32 shares, (M, N) per split
 constexpr int kDecPair = 2;    // silu(gate) * up into C
 constexpr int kDecPairWs = 3;  // gate and up fp32 shares, (M, 2N) per split
+constexpr int kDecArrive = 4;  // fp32 shares, the last split of a block sums them into C
 
 template <int NW, int FN, int MF, int U, int MODE>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
@@ -122,7 +126,54 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(const DecodeArgs p) {
     for (int j = 0; j < FN; ++j) red[wave][i * FN + j][lane] = acc[i][j];
   __syncthreads();
 
-  if constexpr (!PAIR) {
+  if constexpr (MODE == kDecArrive) {
+    // This split's share of the block, then one arrival at the block's counter; the last of
+    // the gridDim.y splits to arrive sums the shares in split order (so the result does not
+    // depend on the order of arrival), applies the epilogue, stores C and sets the counter
+    // back to zero for the next call (the reference's decode split finishes the same way,
+    // python/hk/ops/decode_gemm.py:155-170). The shares are written and read as device-scope
+    // relaxed atomics (coherent across the XCDs' L2s by themselves), and each wave waits for
+    // its share stores before the barrier that precedes the arrival: a device-scope fence
+    // instead writes back and invalidates the whole L2, and with hundreds of workgroups
+    // arriving it made the call 5-100x slower.
+    __shared__ int last;
+    for (int f = wave; f < NF; f += NW) {
+      f32x4 s = red[0][f][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) s += red[w2][f][lane];
+      const int i = f / FN, j = f - i * FN;
+      const int m = i * 16 + rf, n = n0 + j * 16 + 4 * kq;
+      if (m < p.M && n < p.N) {
+        float* dst = p.ws + (int64_t)split * p.split_stride + (int64_t)m * p.N + n;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) __hip_atomic_store(dst + e, s[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // this wave's share stores performed
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(p.cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (int)gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int f = wave; f < NF; f += NW) {
+      const int i = f / FN, j = f - i * FN;
+      const int m = i * 16 + rf, n = n0 + j * 16 + 4 * kq;
+      if (m < p.M && n < p.N) {
+        float* w0 = p.ws + (int64_t)m * p.N + n;
+        f32x4 s;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = __hip_atomic_load(w0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int s2 = 1; s2 < (int)gridDim.y; ++s2) {
+          float* src = w0 + (int64_t)s2 * p.split_stride;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[e] += __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        store4(p.c, p.c_dt, (int64_t)m * p.ldc + n, fused_apply(p.ep, s, m, n, true));
+      }
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (!PAIR) {
     for (int f = wave; f < NF; f += NW) {
       f32x4 s = red[0][f][lane];
 #pragma unroll

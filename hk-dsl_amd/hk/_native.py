@@ -70,11 +70,13 @@ class HkxGemmArgs(Structure):
                 ("kernel", c_int32), ("tile_m", c_int32), ("tile_n", c_int32),
                 ("splits", c_int32), ("tile_schedule", c_int32), ("variant", c_int32),
                 ("decode_waves", c_int32), ("decode_rows", c_int32),
-                ("ws", c_void_p), ("ws_bytes", c_size_t), ("ep", HkxEpilogue)]
+                ("ws", c_void_p), ("ws_bytes", c_size_t), ("ep", HkxEpilogue),
+                ("counters", c_void_p), ("counters_len", c_int64)]
 
 
 #: Every function include/hkx.h declares.
 SYMBOLS = ("hkx_abi_version", "hkx_abi_sizes", "hkx_last_error", "hkx_gemm_workspace",
+           "hkx_gemm_counters",
            "hkx_gemm_check", "hkx_gemm", "hkx_scaled_mm", "hkx_mx_gemm", "hkx_mx_gemm_workspace",
            "hkx_mx_quant", "hkx_gemm_noalloc")
 
@@ -113,6 +115,8 @@ def lib() -> ctypes.CDLL:
         L.hkx_last_error.restype = c_char_p
         L.hkx_gemm_workspace.argtypes = [POINTER(HkxGemmArgs)]
         L.hkx_gemm_workspace.restype = c_size_t
+        L.hkx_gemm_counters.argtypes = [POINTER(HkxGemmArgs)]
+        L.hkx_gemm_counters.restype = c_size_t
         L.hkx_gemm_check.argtypes = [POINTER(HkxGemmArgs)]
         L.hkx_gemm.argtypes = [POINTER(HkxGemmArgs), c_void_p]
         L.hkx_gemm_noalloc.argtypes = [POINTER(HkxGemmArgs), c_void_p]
@@ -202,6 +206,40 @@ def workspace(device, nbytes: int):
     return buf
 
 
+_CNT: dict = {}
+_CNT_GRAPH: dict = {}
+
+
+def counters(device, n: int):
+    """int32 arrival counters (at least `n`, all zero) for a decode call split over K, or
+    None: the reference's per-shape `cnt` (python/hk/ops/decode_gemm.py:283-298), zeroed
+    once when made and kept at zero by the kernel (its last arriver resets its counter).
+
+    Eager calls get a buffer per (device, stream), since calls on one stream run in order.
+    A call under CUDA-graph capture gets the device's graph buffer -- made, zeroed, by an
+    eager call before the capture (e.g. a warm-up), as the reference's is -- and None if no
+    eager call made one: the capture then records the split's two-launch form, with no
+    memset or fill in the graph. Graphs replayed at the same time on several streams of one
+    device share the graph buffer, so such replays must not overlap."""
+    import torch  # noqa: PLC0415
+
+    if n <= 0:
+        return None
+    if capturing(device):
+        buf = _CNT_GRAPH.get(device)
+        return buf if buf is not None and buf.numel() >= n else None
+    key = (device, stream_of(device))
+    buf = _CNT.get(key)
+    if buf is None or buf.numel() < n:
+        size = max(n, 4096)
+        buf = torch.zeros(size, dtype=torch.int32, device=device)
+        _CNT[key] = buf
+        g = _CNT_GRAPH.get(device)
+        if g is None or g.numel() < size:
+            _CNT_GRAPH[device] = torch.zeros(size, dtype=torch.int32, device=device)
+    return buf
+
+
 def gemm_args(a, b, c, *, kernel=KERNEL_AUTO, tile_m=0, tile_n=0, splits=1, schedule=TILE_AUTO,
               variant=0, decode_waves=0, decode_rows=0, ep: HkxEpilogue = None) -> HkxGemmArgs:
     """HkxGemmArgs for A (M, K), B (N, K) -- (2N, K) paired -- and C (M, N) tensors."""
@@ -231,6 +269,10 @@ def run(args: HkxGemmArgs, device) -> None:
     if need:
         ws = workspace(device, need)
         args.ws, args.ws_bytes = ws.data_ptr(), ws.numel() * 4
+    ncnt = L.hkx_gemm_counters(ctypes.byref(args))
+    cnt = counters(device, ncnt) if ncnt and not args.counters else None
+    if cnt is not None:
+        args.counters, args.counters_len = cnt.data_ptr(), cnt.numel()
     check(L.hkx_gemm(ctypes.byref(args), c_void_p(stream_of(device))))
 
 
@@ -246,4 +288,4 @@ def run_noalloc(args: HkxGemmArgs, device) -> None:
 
 
 __all__ = ["lib", "check", "run_noalloc", "NOALLOC_SCRATCH_BYTES", "HkxError", "HkxGemmArgs", "HkxEpilogue", "HkxOperand", "HkxInstr",
-           "gemm_args", "run", "workspace", "dtype_code", "SYMBOLS", "OP", "OPS"]
+           "gemm_args", "run", "workspace", "counters", "dtype_code", "SYMBOLS", "OP", "OPS"]

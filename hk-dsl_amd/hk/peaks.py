@@ -21,7 +21,8 @@ def _lib():
         if not path.is_file():
             raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
         _LIB = ctypes.CDLL(str(path))
-        for f in ("hkxp_mfma", "hkxp_mfma_rand", "hkxp_mfma_issue", "hkxp_read", "hkxp_clock", "hkxp_lds"):
+        for f in ("hkxp_mfma", "hkxp_mfma_rand", "hkxp_mfma_issue", "hkxp_read", "hkxp_read_v",
+                  "hkxp_clock", "hkxp_lds"):
             getattr(_LIB, f).restype = ctypes.c_int
     return _LIB
 
@@ -102,18 +103,33 @@ def mfma_issue_tflops(waves_per_simd: int = 1, device="cuda:0") -> float:
     return blocks * 4 * iters * 8 * (2 * 16 * 16 * 32) / t / 1e12
 
 
-def hbm_read_gbs(nbytes: int = 2 << 30, device="cuda:0") -> float:
-    """GB/s of one pass of 16-byte non-temporal reads over `nbytes` (> the 256 MB MALL)."""
+def hbm_read_gbs(nbytes: int = 1 << 30, nbuf: int = 4, device="cuda:0", detail=False):
+    """GB/s of reads over `nbuf` buffers of `nbytes`, read one after another in rotation
+    (4 x 1 GiB: each buffer is 4x the 256 MB Infinity Cache, so every pass reads HBM), the
+    reference's method (docs/history/42-mi355x-in-the-engine.md:17-22). Three read kernels
+    are timed -- the 16-byte grid-stride read, and 64 KB chunks strided over 8 workgroups a
+    CU with non-temporal or plain loads -- each over 2 rotations (8 launches) bracketed by
+    events, best of 5 after a warm-up; the best kernel is the ceiling. `detail` returns
+    every kernel's figure as well."""
     import torch  # noqa: PLC0415
 
     L = _lib()
-    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=device) for _ in range(nbuf)]
     out = torch.zeros(1, dtype=torch.int32, device=device)
     st = torch.cuda.current_stream(device).cuda_stream
-    t = _time(lambda: L.hkxp_read(ctypes.c_void_p(buf.data_ptr()), ctypes.c_size_t(nbytes),
-                                  ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)))
-    del buf
-    return nbytes / t / 1e9
+    res = {}
+    for v, name in ((0, "grid_stride_nt"), (1, "chunks_64k_nt"), (2, "chunks_64k")):
+        def run():
+            for r in range(2):
+                for b in bufs:
+                    L.hkxp_read_v(v, ctypes.c_void_p(b.data_ptr()), ctypes.c_size_t(nbytes),
+                                  cus * 8, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st))
+        t = _time(run, reps=5)
+        res[name] = 2 * nbuf * nbytes / t / 1e9
+    del bufs
+    best = max(res.values())
+    return (best, res) if detail else best
 
 
 def shader_clock_ghz(device="cuda:0") -> float:
@@ -158,6 +174,7 @@ def measure(device="cuda:0") -> dict:
             "mfma_16x16x32_bf16_two_waves_a_simd_tflops": mfma_issue_tflops(2, device),
             "mfma_fp8_tflops": mfma_tflops(True, device),
             "hbm_read_gbs": hbm_read_gbs(device=device),
+            "hbm_read_method": "4 x 1 GiB buffers read in rotation, best of three read kernels",
             "shader_clock_ghz_mfma_load": shader_clock_ghz(device),
             "lds_read_b128_bytes_per_clk_cu": lds_read_bytes_per_clk(0, device),
             "lds_read_b128_bytes_per_clk_cu_fragment_pattern": lds_read_bytes_per_clk(1, device)}

@@ -572,6 +572,7 @@ class _Launch:
         self.args = args
         self.size = ctypes.sizeof(nat.HkxGemmArgs)
         self.lib = nat.lib()
+        self.ncnt = None  # arrival counters the plan takes (asked once, at the first call)
 
     def __call__(self, a, b, out, operands: Dict[str, Any]):
         if a.stride(1) != 1 or (a.stride(0) * a.element_size()) % 16 or a.data_ptr() % 16:
@@ -595,6 +596,12 @@ class _Launch:
         if need:
             ws = nat.workspace(dev, need)
             args.ws, args.ws_bytes = ws.data_ptr(), ws.numel() * 4
+        if self.ncnt is None:
+            self.ncnt = L.hkx_gemm_counters(ctypes.byref(args))
+        if self.ncnt:
+            cnt = nat.counters(dev, self.ncnt)
+            if cnt is not None:
+                args.counters, args.counters_len = cnt.data_ptr(), cnt.numel()
         nat.check(L.hkx_gemm(ctypes.byref(args), ctypes.c_void_p(nat.stream_of(dev))))
         return out
 

@@ -121,6 +121,28 @@ __global__ void __launch_bounds__(256) read_kernel(const i32x4* p, size_t n16, i
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x12345678) out[0] = 1;
 }
 
+// HBM read in 64 KB chunks strided over the grid: each thread keeps 8 loads of 16 bytes in
+// flight (chunk c of workgroup g: c = g + i G), non-temporal (NT = 1) or plain.
+template <int NT>
+__global__ void __launch_bounds__(512) read_chunks_kernel(const i32x4* p, size_t n16, int* out) {
+  constexpr int U = 8;
+  const size_t per = (size_t)U * 512;  // 16-byte pieces a chunk
+  i32x4 acc = {0, 0, 0, 0};
+  for (size_t c = blockIdx.x; c * per < n16; c += gridDim.x) {
+    const size_t base = c * per + threadIdx.x;
+    i32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t i = base + (size_t)u * 512;
+      if (NT) v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : i32x4{0, 0, 0, 0};
+      else v[u] = i < n16 ? p[i] : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u];
+  }
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x12345678) out[0] = 1;
+}
+
 __global__ void __launch_bounds__(256) clock_kernel(unsigned long long* out, int iters) {
   const unsigned long long t0 = __builtin_amdgcn_s_memtime();
   const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
@@ -208,6 +230,20 @@ int hkxp_mfma_rand(int fp8, int blocks, int iters, float* out, void* stream) {
 int hkxp_read(const void* p, size_t bytes, int* out, void* stream) {
   hipLaunchKernelGGL(read_kernel, dim3(256 * 16), dim3(256), 0, (hipStream_t)stream,
                      (const i32x4*)p, bytes / 16, out);
+  return (int)hipGetLastError();
+}
+
+// variant 0: read_kernel; 1: 64 KB chunks, non-temporal; 2: 64 KB chunks, plain loads
+int hkxp_read_v(int variant, const void* p, size_t bytes, int blocks, int* out, void* stream) {
+  if (variant == 0)
+    hipLaunchKernelGGL(read_kernel, dim3(256 * 16), dim3(256), 0, (hipStream_t)stream,
+                       (const i32x4*)p, bytes / 16, out);
+  else if (variant == 1)
+    hipLaunchKernelGGL(read_chunks_kernel<1>, dim3(blocks), dim3(512), 0, (hipStream_t)stream,
+                       (const i32x4*)p, bytes / 16, out);
+  else
+    hipLaunchKernelGGL(read_chunks_kernel<0>, dim3(blocks), dim3(512), 0, (hipStream_t)stream,
+                       (const i32x4*)p, bytes / 16, out);
   return (int)hipGetLastError();
 }
 

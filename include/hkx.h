@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define HKX_ABI_VERSION 3
+#define HKX_ABI_VERSION 4
 
 /* Status codes. */
 #define HKX_OK 0
@@ -220,6 +220,14 @@ typedef struct HkxGemmArgs {
   void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */
   size_t ws_bytes;
   HkxEpilogue ep;
+  /* DECODE split over K: int32 arrival counters, hkx_gemm_counters() of them, all zero
+     before the first call. With them the blocked decode kernel finishes the split itself:
+     each workgroup stores its fp32 share and arrives at its block's counter, and the last
+     to arrive sums the shares in split order, applies the epilogue and sets the counter
+     back to zero -- one launch. NULL: the shares are summed by a second launch. Calls
+     that overlap in time on one GPU must not share counters. */
+  int32_t* counters;
+  int64_t counters_len;
 } HkxGemmArgs;
 
 /* Library identity. */
@@ -233,6 +241,13 @@ const char* hkx_last_error(void);
 /* Bytes of fp32 workspace hkx_gemm needs for these args (0 if none). Resolves
  * HKX_KERNEL_AUTO the way hkx_gemm does. Host-only, needs no GPU. */
 size_t hkx_gemm_workspace(const HkxGemmArgs* args);
+
+/* int32 arrival counters hkx_gemm uses for these args (0 if the plan has no in-kernel
+ * arrival): the blocked decode kernel split over K, unpaired, fused or no epilogue. Replaces
+ * the counter half of decode_gemm.scratch_for (python/hk/ops/decode_gemm.py:283-298), whose
+ * kernel arrives at cnt[b] and whose last arriver sums, finishes and resets it (:155-170).
+ * Host-only, needs no GPU. */
+size_t hkx_gemm_counters(const HkxGemmArgs* args);
 
 /* Checks args (HKX_OK or an error code, message in hkx_last_error) without launching.
  * Host-only, needs no GPU. */

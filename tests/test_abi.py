@@ -27,7 +27,7 @@ def test_the_library_exports_every_declared_symbol():
     assert set(names) == set(nat.SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.hkx_abi_version() == 3
+    assert L.hkx_abi_version() == 4
 
 
 def test_no_kernel_launch_stub_is_missing():
@@ -147,6 +147,29 @@ def test_workspace_sizes():
     pp = _args(m=2048, n=8192, k=512, tile_m=256, tile_n=256, tile_schedule=nat.TILE_PINGPONG,
                variant=nat.RING_HALFSTAGE)
     assert _check(pp)[0] == nat.ERR_ARG
+
+
+def test_arrival_counter_counts():
+    """hkx_gemm_counters: one int32 a block of decode rows for an unpaired decode call split
+    over K, none otherwise; a call given too few counters is refused before any launch."""
+    L = nat.lib()
+    d = _args(m=16, n=4100, k=4096, kernel=nat.KERNEL_DECODE, splits=4)
+    assert L.hkx_gemm_counters(ctypes.byref(d)) == 257
+    d.decode_rows = 32
+    assert L.hkx_gemm_counters(ctypes.byref(d)) == 129
+    d.splits = 1
+    assert L.hkx_gemm_counters(ctypes.byref(d)) == 0
+    assert L.hkx_gemm_counters(ctypes.byref(_args(splits=2))) == 0  # tile kernels: none
+    pair = _args(m=16, n=4096, k=4096, kernel=nat.KERNEL_DECODE, splits=4, decode_rows=32)
+    pair.ep.form = nat.EP_SILU_MUL
+    assert L.hkx_gemm_counters(ctypes.byref(pair)) == 0
+    short = _args(m=16, n=4100, k=4096, kernel=nat.KERNEL_DECODE, splits=4)
+    short.ws, short.ws_bytes = 0x50000, 1 << 30
+    short.counters, short.counters_len = 0x60000, 100
+    rc, msg = _check(short)
+    assert rc == nat.ERR_WORKSPACE and "counters" in msg
+    short.counters_len = 257
+    assert _check(short)[0] == nat.OK
 
 
 def test_mx_workspace_sizes():
