@@ -331,6 +331,104 @@ def ref_table():
                       "within_10pct": within10, "rows": rows}))
 
 
+ARMS = ["cfg2_bias_gelu", "cfg2_plain", "cfg2_hipblaslt", "cfg2_bias_gelu_zero_x",
+        "cfg5_deq_bias", "cfg5_deq_bias_zero_x", "cfg5_torch_scaled_mm"]
+
+
+def arms():
+    """The workload of the clock-and-cycles profile: config 2 (bias + GELU, plain, hipBLASLt's
+    plain GEMM through torch.matmul, bias + GELU on an all-zero x) and config 5 (dequant +
+    bias, the same on an all-zero x, torch._scaled_mm), each 0.4 s of untimed calls, a
+    50 ms pause, 30 calls, a 50 ms pause -- so a trace splits into the arms by its gaps. Run
+    under rocprofv3 twice: --kernel-trace, and --pmc GRBM_GUI_ACTIVE ...; then
+    `bench.py --arms-summary TRACE_DIR PMC_DIR` prints the table."""
+    import torch
+
+    import hk
+
+    T = hk.templates.gemm
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(4096, 4096, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(12288, 4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(12288, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    y = torch.empty(4096, 12288, device=dev, dtype=torch.bfloat16)
+    zx = torch.zeros_like(x)
+    x8 = torch.randn(8192, 4096, device=dev, generator=g).to(torch.float8_e4m3fn)
+    w8 = torch.randn(4096, 4096, device=dev, generator=g).to(torch.float8_e4m3fn)
+    z8 = torch.zeros_like(x8)
+    sa = (torch.rand(8192, 1, device=dev, generator=g) * 1.5 + 0.5) / 448
+    sb = (torch.rand(4096, device=dev, generator=g) * 1.5 + 0.5) / 448
+    b5 = (torch.randn(4096, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    y5 = torch.empty(8192, 4096, device=dev, dtype=torch.bfloat16)
+    sm = hk.ops.scaled_mm
+    fns = [lambda: T(x, w, epilogue=T.bias_gelu, bias=b, out=y),
+           lambda: T(x, w, out=y),
+           lambda: torch.matmul(x, w.t(), out=y),
+           lambda: T(zx, w, epilogue=T.bias_gelu, bias=b, out=y),
+           lambda: sm(x8, w8, sa, sb, bias=b5, out=y5),
+           lambda: sm(z8, w8, sa, sb, bias=b5, out=y5),
+           lambda: torch._scaled_mm(x8, w8.t(), scale_a=sa, scale_b=sb.reshape(1, -1),
+                                    out_dtype=torch.bfloat16)]
+    for name, fn in zip(ARMS, fns):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.4:
+            fn()
+        torch.cuda.synchronize()
+        time.sleep(0.05)
+        for _ in range(30):
+            fn()
+        torch.cuda.synchronize()
+        time.sleep(0.05)
+        print(name, flush=True)
+
+
+def arms_summary(trace_dir, pmc_dir):
+    """The clock-and-cycles table from the two rocprofv3 runs of `arms`: per arm, the
+    median kernel time of its 30 timed calls (kernel trace), the median GRBM_GUI_ACTIVE of
+    the same calls divided by the 8 XCDs (the counter sums them) -- cycles a launch --,
+    their ratio (the clock the launch ran at), and the fraction of the datasheet peak at
+    that clock and at 2.4 GHz (the cycles alone)."""
+    import collections
+    import csv
+
+    def gemm(name):
+        return "quad" in name or "Cijk" in name
+
+    def by_gap(items, st, en):
+        out, last = [], None
+        for it in items:
+            if last is None or st(it) - last > 20e6:
+                out.append([])
+            out[-1].append(it)
+            last = en(it)
+        return out[1::2]  # each arm: its untimed calls, then (after the pause) the 30 timed
+
+    rows = sorted((r for r in csv.DictReader(open(os.path.join(trace_dir, "run_kernel_trace.csv")))
+                   if gemm(r["Kernel_Name"])), key=lambda r: int(r["Start_Timestamp"]))
+    tarms = by_gap(rows, lambda r: int(r["Start_Timestamp"]), lambda r: int(r["End_Timestamp"]))
+    disp = collections.OrderedDict()
+    for r in csv.DictReader(open(os.path.join(pmc_dir, "run_counter_collection.csv"))):
+        if gemm(r["Kernel_Name"]):
+            e = disp.setdefault(int(r["Dispatch_Id"]), {"st": int(r["Start_Timestamp"]),
+                                                         "en": int(r["End_Timestamp"]),
+                                                         "c": collections.Counter()})
+            e["c"][r["Counter_Name"]] += float(r["Counter_Value"])
+    carms = by_gap(sorted(disp.values(), key=lambda e: e["st"]), lambda e: e["st"], lambda e: e["en"])
+    flops = {"cfg2": 2.0 * 4096 * 4096 * 12288, "cfg5": 2.0 * 8192 * 4096 * 4096}
+    peak = {"cfg2": PEAK_BF16 * 1e12, "cfg5": PEAK_FP8 * 1e12}
+    print("| arm | kernel | median µs | cycles a launch | clock GHz | frac of peak | frac at 2.4 GHz |")
+    print("|---|---|---:|---:|---:|---:|---:|")
+    for name, ta, ca in zip(ARMS, tarms, carms):
+        us = statistics.median((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in ta[-30:])
+        cyc = statistics.median(c["c"]["GRBM_GUI_ACTIVE"] for c in ca[-30:]) / 8
+        kn = ta[-1]["Kernel_Name"]
+        kn = kn[:kn.find("(")] if "(" in kn else kn[:48]
+        f, pk = flops[name[:4]], peak[name[:4]]
+        print(f"| {name} | `{kn}` | {us:.1f} | {cyc / 1e3:.0f} K | {cyc / us / 1e3:.2f} | "
+              f"{f / (us * 1e-6) / pk:.3f} | {f / (cyc / 2.4e9) / pk:.3f} |")
+
+
 def main():
     global RAMP_S
     ap = argparse.ArgumentParser()
@@ -344,8 +442,18 @@ def main():
                     help="also run a 1 GiB device copy (the scale of rocprof's FETCH/WRITE_SIZE)")
     ap.add_argument("--ref-table", action="store_true",
                     help="time the reference's published template table instead (one JSON line)")
+    ap.add_argument("--arms", action="store_true",
+                    help="run the clock-and-cycles profile's workload instead (see arms)")
+    ap.add_argument("--arms-summary", nargs=2, metavar=("TRACE_DIR", "PMC_DIR"),
+                    help="print the clock-and-cycles table from two rocprofv3 runs of --arms")
     args = ap.parse_args()
     RAMP_S = args.ramp
+    if args.arms_summary:
+        arms_summary(*args.arms_summary)
+        return
+    if args.arms:
+        arms()
+        return
     if args.ref_table:
         ref_table()
         return
