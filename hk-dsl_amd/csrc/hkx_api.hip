@@ -326,6 +326,21 @@ int make_plan(const HkxGemmArgs* a, Plan* p) {
   }
   p->ncnt = 0;
   p->arrive = false;
+  // the 4-wave tile kernel (which runs every split call of the W4 schedule and of the
+  // ring schedule's 128-row tiles) finishes its split itself: a counter a tile
+  // (a share's byte offsets fit 32 bits)
+  const bool tile4_split = kernel == HKX_KERNEL_TILE && p->splits > 1 && !pair && !program &&
+                           p->sk_splits == 0 && (long long)p->splits * a->m * a->n * 4 < (1LL << 32) &&
+                           (p->schedule == HKX_TILE_W4 || (p->schedule == HKX_TILE_RING && p->tile_m == 128));
+  if (tile4_split) {
+    p->ncnt = ((a->m + p->tile_m - 1) / p->tile_m) * ((a->n + p->tile_n - 1) / p->tile_n);
+    if (a->counters) {
+      if (a->counters_len < p->ncnt || !aligned(a->counters, 4))
+        return fail(HKX_ERR_WORKSPACE, "this plan needs %d 4-byte aligned arrival counters "
+                    "(counters_len %lld)", p->ncnt, (long long)a->counters_len);
+      p->arrive = true;
+    }
+  }
   if (kernel == HKX_KERNEL_DECODE && p->splits > 1 && !pair && !program) {
     p->ncnt = (a->n + 16 * p->fn - 1) / (16 * p->fn);
     if (a->counters) {
@@ -567,6 +582,13 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       t.ep = hkx::Fused{};
       t.ep.form = HKX_EP_NONE;
       mode = p.pair ? hkx::kPairWs : hkx::kStoreF32;
+      if (p.arrive) {  // the last split of each tile finishes it into C
+        t.cnt = a.counters;
+        t.fin_c = a.c;
+        t.fin_ldc = a.ldc;
+        t.fin_dt = a.c_dtype;
+        t.fin_ep = fused;
+      }
     } else {
       t.c = a.c;
       t.ldc = a.ldc;

@@ -57,6 +57,15 @@ struct TileArgs {
   // fp8 operand formats: 1 e4m3 x e4m3, 2 e5m2 x e5m2, 3 A e4m3 x B e5m2, 4 A e5m2 x B e4m3
   // (0 for bf16); formats past 1 run on the ring kernel only
   int32_t ab_fmt;
+  // A K split finished in the kernel (MODE kStoreF32 with split shares): one arrival
+  // counter a tile (blockIdx.x), zero before the call and left at zero; the last split to
+  // arrive sums the shares into fin_c (row stride fin_ldc, type fin_dt) with fin_ep.
+  // cnt == nullptr: the shares stay for the reduction pass.
+  int32_t* cnt;
+  void* fin_c;
+  int64_t fin_ldc;
+  int32_t fin_dt;
+  Fused fin_ep;
 };
 
 // How a tile leaves the kernel.
@@ -67,6 +76,97 @@ constexpr int kPair16 = 3;    // silu(gate) * up, 16-bit C, through LDS staging
 constexpr int kPairWs = 4;    // gate and up fp32 shares, (M, 2N) per split
 
 HKX_DEV int swz(int j) { return (j ^ (j >> 3)) & 7; }
+
+// A split share's four fp32 values, stored and loaded through a buffer resource over the
+// split's share with the device-scope coherence bit (sc1, cache policy 16): coherent
+// across the XCDs' L2s without a cache-wide fence, which a workgroup's finish of a split
+// cannot afford (a device-scope fence writes back and invalidates the whole L2). Byte
+// offsets from the share's start, which the host keeps under 4 GiB.
+constexpr int kCpolSc1 = 16;
+
+HKX_DEV void share_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, off, 0, kCpolSc1);
+}
+
+HKX_DEV f32x4 share_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
+}
+
+// After a workgroup stored its split's share of tile `tile` (rows m0.., columns n0.. of
+// a BM x OW tile; NT threads): its arrival at the tile's counter, and, if it is the last
+// of the gridDim.y splits, the tile's finish -- the shares summed in split order (the
+// reduction pass's order, so the result does not depend on which split arrives last),
+// the fused epilogue, the store, and the counter back to zero for the next call. Every
+// thread of the workgroup calls it. The reference finishes its stream-K and decode splits
+// the same way (python/hk/ops/gemm_cdna.py:421-496, python/hk/ops/decode_gemm.py:155-170).
+// The finish's sums and stores with S (a compile-time split count, or 0: run time) shares:
+// each thread takes groups tid, tid + NT, ... of four columns and issues the loads of up to
+// 16 share pieces before adding any (so it waits a memory latency per 16 loads, not one a
+// group: issued group by group, the finish of a 64 x 128 tile split 4 ways cost 9 us).
+template <int BM, int OW, int NT, int S>
+HKX_DEV void finish_sums(const TileArgs& p, __amdgpu_buffer_rsrc_t r, uint32_t sb, int m0, int n0) {
+  constexpr int IT = BM * OW / 4 / NT;  // groups a thread
+  constexpr int SS = S > 0 ? S : 1;
+  constexpr int CH = S == 0 ? 1 : ((16 / SS) < 1 ? 1 : ((16 / SS) > IT ? IT : 16 / SS));
+  const int splits = S > 0 ? S : (int)gridDim.y;
+  for (int base = 0; base < IT; base += CH) {
+    f32x4 x[CH][SS];
+    uint32_t off[CH];
+    bool ok[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int q = (int)threadIdx.x + (base + c) * NT;
+      const int row = q / (OW / 4), c4 = q - row * (OW / 4);
+      const int m = m0 + row, n = n0 + 4 * c4;
+      ok[c] = base + c < IT && m < p.M && n < p.N;
+      off[c] = ((uint32_t)m * (uint32_t)p.ldc + (uint32_t)n) * 4u;
+      if constexpr (S > 0) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) x[c][s] = ok[c] ? share_load4(r, off[c] + (uint32_t)s * sb) : f32x4{};
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (!ok[c]) continue;
+      f32x4 v;
+      if constexpr (S > 0) {
+        v = x[c][0];
+#pragma unroll
+        for (int s = 1; s < S; ++s) v += x[c][s];
+      } else {
+        v = share_load4(r, off[c]);
+        for (int s = 1; s < splits; ++s) v += share_load4(r, off[c] + (uint32_t)s * sb);
+      }
+      const int q = (int)threadIdx.x + (base + c) * NT;
+      const int row = q / (OW / 4), c4 = q - row * (OW / 4);
+      const int m = m0 + row, n = n0 + 4 * c4;
+      v = fused_apply(p.fin_ep, v, m, n, true);
+      store4(p.fin_c, p.fin_dt, (int64_t)m * p.fin_ldc + n, v);
+    }
+  }
+}
+
+template <int BM, int OW, int NT>
+HKX_DEV void finish_split(const TileArgs& p, int tile, int m0, int n0, int* last) {
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): this wave's share stores performed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *last = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (int)gridDim.y - 1;
+  __syncthreads();
+  if (!*last) return;
+  // (the host keeps all the shares, splits x split_stride floats, under 4 GiB)
+  const uint32_t sb = (uint32_t)p.split_stride * 4u;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(p.c, sb * (uint32_t)gridDim.y);
+  switch (gridDim.y) {
+    case 2: finish_sums<BM, OW, NT, 2>(p, r, sb, m0, n0); break;
+    case 3: finish_sums<BM, OW, NT, 3>(p, r, sb, m0, n0); break;
+    case 4: finish_sums<BM, OW, NT, 4>(p, r, sb, m0, n0); break;
+    case 8: finish_sums<BM, OW, NT, 8>(p, r, sb, m0, n0); break;
+    default: finish_sums<BM, OW, NT, 0>(p, r, sb, m0, n0); break;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The swizzle of rows of four 16-byte chunks (64-byte half-stage rows): chunk c of row r is
 // stored at c ^ swz4(r), bits 4 and 3 of the row, which makes the fragment reads of 32

@@ -59,7 +59,10 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   static_assert(SMEM <= 160 * 1024, "LDS");
   using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+  // (+16 bytes: the split finish's flag. A second __shared__ object would make the compiler
+  // wait for every LDS-DMA fill before each LDS read: it could no longer tell the fills'
+  // destination from the flag, and the main loop ran 2x slower)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM + 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -289,6 +292,8 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
   const int nw = wn * TN + 4 * h;
   if constexpr (MODE == kStoreF32 || MODE == kPairWs) {
     float* out = (float*)p.c + (int64_t)split * p.split_stride;
+    // (a share finished in the kernel goes out through its buffer, coherent device-wide)
+    const __amdgpu_buffer_rsrc_t rshare = make_rsrc(out, (uint32_t)p.M * (uint32_t)p.ldc * 4u);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + mw + 32 * i;
@@ -308,7 +313,8 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
                 if (e.ta.p) v += ld_tile(e.ta, m, n);
                 v = act4(e.act, v + e.cadd);
               }
-              *(f32x4*)(out + (int64_t)m * p.ldc + n) = v;
+              if (p.cnt) share_store4(rshare, ((uint32_t)m * (uint32_t)p.ldc + (uint32_t)n) * 4u, v);
+              else *(f32x4*)(out + (int64_t)m * p.ldc + n) = v;
             }
           } else {
             const int fv = wn * FN + j;
@@ -317,6 +323,9 @@ __global__ void __launch_bounds__(256, 1) tile4_kernel(const TileArgs p) {
               *(f32x4*)(out + (int64_t)m * p.ldc + oc + ((fv & 1) ? p.N : 0)) = v;
           }
         }
+    }
+    if constexpr (MODE == kStoreF32) {
+      if (p.cnt) finish_split<BM, OUTW, 256>(p, blockIdx.x, m0, n0, (int*)(smem + SMEM));
     }
   } else {
     __syncthreads();  // the stages are reused as the staging tile

@@ -269,7 +269,9 @@ def run(args: HkxGemmArgs, device) -> None:
     if need:
         ws = workspace(device, need)
         args.ws, args.ws_bytes = ws.data_ptr(), ws.numel() * 4
-    ncnt = L.hkx_gemm_counters(ctypes.byref(args))
+    # arrival counters for a decode split (one launch instead of two, measured level with
+    # them); a tile kernel's split keeps its reduction launch, which measured faster
+    ncnt = L.hkx_gemm_counters(ctypes.byref(args)) if args.kernel == KERNEL_DECODE else 0
     cnt = counters(device, ncnt) if ncnt and not args.counters else None
     if cnt is not None:
         args.counters, args.counters_len = cnt.data_ptr(), cnt.numel()

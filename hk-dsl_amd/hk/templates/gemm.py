@@ -597,7 +597,11 @@ class _Launch:
             ws = nat.workspace(dev, need)
             args.ws, args.ws_bytes = ws.data_ptr(), ws.numel() * 4
         if self.ncnt is None:
-            self.ncnt = L.hkx_gemm_counters(ctypes.byref(args))
+            # a decode split finishes in the kernel (one launch; measured level with the
+            # two-launch form); a tile split keeps its reduction launch (the in-kernel finish
+            # of the 4-wave kernel measured 4-10 us slower at M = 16-128)
+            self.ncnt = (L.hkx_gemm_counters(ctypes.byref(args))
+                         if args.kernel == nat.KERNEL_DECODE else 0)
         if self.ncnt:
             cnt = nat.counters(dev, self.ncnt)
             if cnt is not None:

@@ -220,12 +220,17 @@ typedef struct HkxGemmArgs {
   void* ws;         /* fp32 workspace, hkx_gemm_workspace() bytes */
   size_t ws_bytes;
   HkxEpilogue ep;
-  /* DECODE split over K: int32 arrival counters, hkx_gemm_counters() of them, all zero
-     before the first call. With them the blocked decode kernel finishes the split itself:
-     each workgroup stores its fp32 share and arrives at its block's counter, and the last
-     to arrive sums the shares in split order, applies the epilogue and sets the counter
-     back to zero -- one launch. NULL: the shares are summed by a second launch. Calls
-     that overlap in time on one GPU must not share counters. */
+  /* A split over K finished in the kernel: int32 arrival counters, hkx_gemm_counters() of
+     them, all zero before the first call. With them the blocked decode kernel (one counter
+     a block of rows) and the 4-wave tile kernel (one a tile) finish the split themselves:
+     each workgroup stores its fp32 share and arrives at its counter, and the last to arrive
+     sums the shares in split order (as the second launch does, so the result is the same),
+     applies the epilogue and sets the counter back to zero -- one launch. NULL: the shares
+     are summed by a second launch. Measured on MI355X, the decode finish costs what the
+     second launch does, the tile finish 4-10 us more a call at M = 16-128 (its last
+     arrivers' chain of share stores, arrival and share loads is all tail); hk's Python
+     layer passes counters for decode splits only. Calls that overlap in time on one GPU
+     must not share counters. */
   int32_t* counters;
   int64_t counters_len;
 } HkxGemmArgs;
@@ -243,7 +248,8 @@ const char* hkx_last_error(void);
 size_t hkx_gemm_workspace(const HkxGemmArgs* args);
 
 /* int32 arrival counters hkx_gemm uses for these args (0 if the plan has no in-kernel
- * arrival): the blocked decode kernel split over K, unpaired, fused or no epilogue. Replaces
+ * arrival): the blocked decode kernel or the 4-wave tile kernel split over K, unpaired,
+ * fused or no epilogue (the tile kernel: all the shares under 4 GiB). Replaces
  * the counter half of decode_gemm.scratch_for (python/hk/ops/decode_gemm.py:283-298), whose
  * kernel arrives at cnt[b] and whose last arriver sums, finishes and resets it (:155-170).
  * Host-only, needs no GPU. */

@@ -151,7 +151,8 @@ def test_workspace_sizes():
 
 def test_arrival_counter_counts():
     """hkx_gemm_counters: one int32 a block of decode rows for an unpaired decode call split
-    over K, none otherwise; a call given too few counters is refused before any launch."""
+    over K, one a tile for the 4-wave tile kernel split over K, none otherwise; a call given
+    too few counters is refused before any launch."""
     L = nat.lib()
     d = _args(m=16, n=4100, k=4096, kernel=nat.KERNEL_DECODE, splits=4)
     assert L.hkx_gemm_counters(ctypes.byref(d)) == 257
@@ -159,7 +160,10 @@ def test_arrival_counter_counts():
     assert L.hkx_gemm_counters(ctypes.byref(d)) == 129
     d.splits = 1
     assert L.hkx_gemm_counters(ctypes.byref(d)) == 0
-    assert L.hkx_gemm_counters(ctypes.byref(_args(splits=2))) == 0  # tile kernels: none
+    # the 4-wave tile kernel split over K: one a tile; the 256 x 256 ring tiles: none
+    assert L.hkx_gemm_counters(ctypes.byref(_args(m=300, n=1000, splits=2))) == 3 * 4
+    ring = _args(m=512, n=512, k=512, tile_m=256, tile_n=256, tile_schedule=nat.TILE_RING, splits=2)
+    assert L.hkx_gemm_counters(ctypes.byref(ring)) == 0
     pair = _args(m=16, n=4096, k=4096, kernel=nat.KERNEL_DECODE, splits=4, decode_rows=32)
     pair.ep.form = nat.EP_SILU_MUL
     assert L.hkx_gemm_counters(ctypes.byref(pair)) == 0

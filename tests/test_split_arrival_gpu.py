@@ -1,11 +1,12 @@
-"""The blocked decode kernel split over K, finished in the kernel: each workgroup stores its
-fp32 share and arrives at its block's counter; the last to arrive sums the shares in split
-order, applies the epilogue and resets the counter (the reference's decode split,
-python/hk/ops/decode_gemm.py:155-170, 283-298). Against the CPU oracle: back-to-back calls
-on the same counters with new inputs, ragged M and N, 16- and 32-row blocks, one and two
-16-token fragments, the fused epilogue forms; the counters are zero after every call; the
-two-launch form (no counters) gives the same values; and a captured graph replayed with new
-inputs uses the counters made by the eager warm-up."""
+"""K splits finished in the kernel: each workgroup stores its fp32 share and arrives at its
+block's (decode) or tile's (4-wave tile kernel) counter; the last to arrive sums the shares
+in split order, applies the epilogue and resets the counter (the reference's decode split,
+python/hk/ops/decode_gemm.py:155-170, 283-298, and stream-K fix-up,
+python/hk/ops/gemm_cdna.py:421-496). Against the CPU oracle: back-to-back calls on the
+same counters with new inputs, ragged M and N, the kernels' tile and block shapes, the
+fused epilogue forms; the counters are zero after every call; the two-launch form (no
+counters) gives the same values; and a captured graph replayed with new inputs uses the
+counters made by the eager warm-up."""
 
 import ctypes
 
@@ -78,6 +79,7 @@ def _launch(args, with_counters):
         ncnt = L.hkx_gemm_counters(ctypes.byref(args))
         assert ncnt > 0
         cnt = nat.counters(torch.device(DEV), ncnt)
+        assert cnt is not None, "no counters made before this capture"
         args.counters, args.counters_len = cnt.data_ptr(), cnt.numel()
     nat.check(L.hkx_gemm(ctypes.byref(args), ctypes.c_void_p(nat.stream_of(torch.device(DEV)))))
     return cnt
@@ -160,4 +162,95 @@ def test_captured_graph_replays_with_the_warm_up_counters():
                        rtol=1e-2, atol=1e-2)
         assert int(gcnt.abs().sum()) == 0
         call()  # eager work between the replays
+        torch.cuda.synchronize()
+
+
+TILE_CASES = [  # m, n, k, tile_m, tile_n, schedule, splits
+    (128, 4096, 4096, 64, 128, nat.TILE_W4, 2), (128, 1000, 4096, 64, 128, nat.TILE_W4, 8),
+    (300, 2048, 3072, 128, 128, nat.TILE_W4, 3), (64, 512, 8192, 64, 256, nat.TILE_W4, 4),
+    (257, 768, 2048, 128, 256, nat.TILE_RING, 2), (16, 4100, 14336, 64, 128, nat.TILE_W4, 7)]
+
+
+def _tile_args(a, b, c, ep, tm, tn, sched, splits):
+    return nat.gemm_args(a, b, c, kernel=nat.KERNEL_TILE, tile_m=tm, tile_n=tn,
+                         schedule=sched, splits=splits, ep=ep)
+
+
+@pytest.mark.parametrize("form", ["none", "bias", "bias_gelu", "residual"])
+@pytest.mark.parametrize("case", TILE_CASES,
+                         ids=[f"{c[0]}x{c[1]}x{c[2]}t{c[3]}x{c[4]}s{c[5]}k{c[6]}" for c in TILE_CASES])
+def test_split_tiles_finish_in_the_kernel(case, form):
+    m, n, k, tm, tn, sched, splits = case
+    print(f"case: tile arrival M={m} N={n} K={k} tile {tm}x{tn} sched {sched} splits {splits} {form}",
+          flush=True)
+    for call in range(2):
+        a, b, bias, r = _data(m, n, k, seed=20 + call)
+        ad, bd, biasd, rd = a.to(DEV), b.to(DEV), bias.to(DEV), r.to(DEV)
+        c = torch.full((m, n + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+        ep, _keep = _ep(form, biasd, rd)
+        cnt = _launch(_tile_args(ad, bd, c[:, :n], ep, tm, tn, sched, splits), with_counters=True)
+        torch.cuda.synchronize()
+        O.assert_close(c[:, :n], _ref(form, a, b, bias, r), rtol=1e-2, atol=1e-2)
+        assert (c[:, n:].float() == 7.0).all()
+        assert int(cnt.abs().sum()) == 0, "a counter was left non-zero"
+        c2 = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        ep2, _keep2 = _ep(form, biasd, rd)
+        _launch(_tile_args(ad, bd, c2, ep2, tm, tn, sched, splits), with_counters=False)
+        torch.cuda.synchronize()
+        assert torch.equal(c[:, :n], c2)
+
+
+def test_split_tiles_fp32_and_int8_outputs():
+    """The finish's store in the other output types: fp32 (unrounded) and int8 (one
+    quantizer step of the oracle's)."""
+    m, n, k = 128, 1024, 4096
+    a, b, bias, r = _data(m, n, k, seed=30)
+    ad, bd = a.to(DEV), b.to(DEV)
+    acc = O.gemm_fp32(a, b)
+    c32 = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    ep, _ = _ep("none", None, None)
+    _launch(_tile_args(ad, bd, c32, ep, 64, 128, nat.TILE_W4, 4), with_counters=True)
+    torch.cuda.synchronize()
+    assert O.rel_to_max(c32.cpu(), acc) < 1e-5
+    c8 = torch.empty((m, n), dtype=torch.int8, device=DEV)
+    ep8, _ = _ep("none", None, None)
+    ep8.form = nat.EP_FUSED
+    ep8.cmul = 20.0
+    _launch(_tile_args(ad, bd, c8, ep8, 64, 128, nat.TILE_W4, 4), with_counters=True)
+    torch.cuda.synchronize()
+    want = O.quantize_int8(acc * 20.0)
+    assert (c8.cpu().int() - want.int()).abs().max() <= 1
+
+
+def test_split_tiles_in_a_captured_graph():
+    m, n, k = 128, 4096, 4096
+    a, b, bias, r = _data(m, n, k, seed=40)
+    ad, bd, biasd = a.to(DEV), b.to(DEV), bias.to(DEV)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    ep, _keep = _ep("bias_gelu", biasd, None)
+
+    def call():  # hk's Python layer leaves a tile split to its reduction launch: counters by hand
+        _launch(_tile_args(ad, bd, c, ep, 64, 128, nat.TILE_W4, 4), with_counters=True)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    gcnt = nat._CNT_GRAPH[torch.device(DEV)]
+    for rep in range(3):
+        a2, b2, bias2, _ = _data(m, n, k, seed=50 + rep)
+        ad.copy_(a2.to(DEV))
+        bd.copy_(b2.to(DEV))
+        biasd.copy_(bias2.to(DEV))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        O.assert_close(c, O.gelu_tanh(O.gemm_fp32(a2, b2) + bias2.float()), rtol=1e-2, atol=1e-2)
+        assert int(gcnt.abs().sum()) == 0
+        call()
         torch.cuda.synchronize()
