@@ -591,7 +591,9 @@ def measured_peaks():
 
 
 def other_configs(steps, warmup, peaks):
-    """Configs 3-5, timed as config 2 is (HIP events per launch, mean)."""
+    """Configs 3-5: configs 3 and 5 timed as config 2 is (HIP events per launch, mean, for
+    the kernel; and K calls back to back, as config 2's value), config 4 from replayed
+    graphs (its launches are shorter than the host's call overhead)."""
     import torch
 
     import hk
@@ -617,9 +619,12 @@ def other_configs(steps, warmup, peaks):
     for m in (2048, 8192):
         x, wt, _ = _inputs(m, 4096, 24576, 3, dev)
         y = torch.empty(m, 12288, device=dev, dtype=torch.bfloat16)
-        t, _, _ = _events_time(lambda: T(x, wt, epilogue=T.silu_and_mul, out=y), steps, warmup)
+        f3 = lambda: T(x, wt, epilogue=T.silu_and_mul, out=y)  # noqa: E731
+        t, _, _ = _events_time(f3, steps, warmup)
+        tw = _wall_time(f3, steps, 0) / steps  # back to back, as config 2's value
         fl = 2.0 * m * 24576 * 4096
         out[f"cfg3_gate_up_silu_mul_M{m}"] = {"TFLOP/s": round(fl / t / 1e12, 1),
+                                              "TFLOP/s_back_to_back": round(fl / tw / 1e12, 1),
                                               "frac_bf16_peak": round(fl / t / 1e12 / PEAK_BF16, 4),
                                               "frac_measured": round(fl / t / 1e12 / peaks["mfma_bf16_tflops"], 4),
                                               "frac_measured_random_operands": round(
@@ -654,9 +659,13 @@ def other_configs(steps, warmup, peaks):
     sb = ((torch.rand(4096, generator=g) * 1.5 + 0.5) / 448).to(dev)
     bias = (torch.randn(4096, generator=g) * 0.1).to(torch.bfloat16).to(dev)
     y = torch.empty(8192, 4096, device=dev, dtype=torch.bfloat16)
-    t, _, _ = _events_time(lambda: hk.ops.scaled_mm(x8, w8, sa, sb, bias=bias, out=y), steps, warmup)
+    f5 = lambda: hk.ops.scaled_mm(x8, w8, sa, sb, bias=bias, out=y)  # noqa: E731
+    t, _, _ = _events_time(f5, steps, warmup)
+    tw = _wall_time(f5, steps, 0) / steps  # back to back, as config 2's value
     fl = 2.0 * 8192 * 4096 * 4096
     out["cfg5_fp8_scaled_dequant_bias"] = {"TFLOP/s": round(fl / t / 1e12, 1),
+                                           "TFLOP/s_back_to_back": round(fl / tw / 1e12, 1),
+                                           "us_back_to_back": round(tw * 1e6, 1),
                                            "frac_fp8_peak": round(fl / t / 1e12 / PEAK_FP8, 4),
                                            "frac_measured": round(fl / t / 1e12 / peaks["mfma_fp8_tflops"], 4),
                                            "frac_measured_random_operands": round(

@@ -717,7 +717,10 @@ int hkx_gemm(const HkxGemmArgs* args, void* stream) {
       d.ep = fused;
       mode = p.pair ? hkx::kDecPair : hkx::kDecOut;
     }
-    if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair) && hkx::rows_takes(d)) {
+    const int gw = std::min((a.n + 7) / 8, cu_count());
+    if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair) && hkx::roww_takes(d, gw)) {
+      rc = launched(hkx::launch_roww(d, dim3(gw), s), "decode GEMM");
+    } else if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair) && hkx::rows_takes(d)) {
       const dim3 g(std::min((a.n + 3) / 4, cu_count()));
       rc = launched(hkx::launch_rows(d, g, s), "decode GEMM");
     } else if ((p.variant & HKX_DEC_STREAM) && hkx::stream_takes(d, p.splits, p.pair)) {

@@ -296,6 +296,189 @@ __global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
   __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // no fill lands in LDS after the exit
 }
 
+// The per-wave whole-row decode GEMM: K = 512 KS (KS = 2 or 4: K = 1024 or 2048), M <= 2
+// (M <= 3 at K = 1024), the fast epilogue form without a tile operand. The workgroups take chunks of 8
+// consecutive rows of W strided over the grid (workgroup g: chunks g, g + G, ...), and wave w
+// takes row w of each: it streams its own rows into its own two LDS slots (a row is 2K
+// bytes, one DMA instruction a KB), so no wave waits for another -- there is no barrier in
+// the kernel. A row's whole K goes through one MFMA chain: the 16 rows of the MFMA are the
+// row's 16 K segments (K / 16 each), and X enters as 16 columns, the same 16 segments of one
+// token, so the row's dot product with the token is the trace of the 16 x 16 result -- the
+// sum of one component in each of 16 lanes. Each row's result (the epilogue applied) waits in
+// the lane of its index; all of a wave's rows are stored at the end, after its last fill
+// (a store among the fills would enter the waits, which count loads and stores together).
+// Against the whole-row kernel above, this removes the per-chunk barrier and the cross-wave
+// sums of each group (and their tail after the last chunk). Measured on one box against the
+// kernels that take these calls otherwise (graph replays over four rotated weights): at K =
+// 1024 and 2048, M <= 2, 5-20% faster (12288 x 1024 at M = 1: 7.76 -> 6.23 us; 24576 x 2048:
+// 18.16 -> 16.45); at K = 4096 (KS = 8, 160 KB of LDS) level at M = 1 and up to 10% slower from
+// M = 2 and at N past 12288 -- there the whole-row kernel above stays. With more tokens each
+// row's MFMA chains and trace sums lengthen the walk, and only two rows a wave are in flight.
+//
+// LDS: wave w's slots at 2 w RB and (2 w + 1) RB, RB = 2K bytes. A row's 16-byte pieces are
+// XOR-swizzled within each 256-byte block by the block's segment (applied on the global side
+// of the DMA), so the 16 lanes reading one k-step of the 16 segments hit 16 different banks.
+template <int KS>
+__device__ __forceinline__ uint32_t roww_swz(uint32_t piece) {  // physical <-> logical piece
+  const uint32_t h = piece >> 4;  // its 256-byte block
+  const uint32_t f = KS == 8 ? (h >> 1) & 15u : (KS == 4 ? h & 15u : h & 7u);
+  return piece ^ f;
+}
+
+template <int KS>
+__global__ void __launch_bounds__(512) roww_kernel(const DecodeArgs p) {
+  constexpr int RB = KS * 1024;  // a row's bytes (K = 512 KS bf16)
+  constexpr int MT = 4;          // tokens at most
+  constexpr int XOFF = 16 * RB;  // then X: MT rows of RB bytes, laid out as W's rows
+  __shared__ __attribute__((aligned(16))) uint8_t ring[XOFF + MT * RB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nck = (p.N + 7) / 8;
+  const int G = gridDim.x, g = blockIdx.x;
+  if (g >= nck) return;  // (no barrier anywhere below)
+  const int nq = (nck - g + G - 1) / G;  // rows of this wave: 8 (g + q G) + wave
+  auto row_of = [&](int q) { return 8 * (g + q * G) + wave; };
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, p.a_bytes);
+  const Fused& e = p.ep;
+  const bool fused = e.form == HKX_EP_FUSED;
+  const bool ra_vec = fused && e.ra.p && e.ra.ld;
+  const float cs_sc = (fused && e.cs.p) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : (fused ? e.cmul : 1.0f);
+  const float rs_sc = (fused && e.rs.p) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
+  const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
+  const float sc = cs_sc * rs_sc;
+  const float add0 = ra_sc + e.cadd;
+
+  // the fragment offsets within a slot: lane l reads segment l % 16, k-group l / 16
+  uint32_t fo[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k)
+    fo[k] = roww_swz<KS>((uint32_t)((lane & 15) * 4 * KS + k * 4 + (lane >> 4))) * 16u;
+  // the DMA's per-lane global offsets: instruction u's lane fills physical piece 64 u + l
+  uint32_t dv[KS];
+#pragma unroll
+  for (int u = 0; u < KS; ++u) dv[u] = roww_swz<KS>((uint32_t)(64 * u + lane)) * 16u;
+  // Row q into slot q & 1; past the last row the fill is still issued, out of range (it reads
+  // nothing and writes a slot already read), so every step waits for the same count.
+  auto fill = [&](int q) {
+    const uint32_t base = q < nq ? (uint32_t)row_of(q) * p.ldb_b : 0x80000000u;
+    uint8_t* slot = ring + (2 * wave + (q & 1)) * RB;
+#pragma unroll
+    for (int u = 0; u < KS; ++u) buf_load16_lds<kNonTemporal>(rw, slot + u * 1024, dv[u] + base, 0);
+  };
+  // the biases of this wave's rows, row q's in lane q, loaded with X before the first fill
+  // (a load in the loop would make the compiler wait for every fill in flight)
+  float bias_l = 0.f;
+  if (ra_vec && lane < nq && row_of(lane) < p.N) bias_l = ld1(e.ra.p, HKX_BF16, row_of(lane));
+  // the rows' results, row q's in lane q (token t in res[t])
+  float res[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) res[t] = 0.f;
+  const bool diag = ((lane & 15) >> 2) == (lane >> 4);  // lanes holding a trace element
+  // X: staged once a workgroup, by wave 0's DMA, in W's row layout (its M rows; rows past M
+  // read zero), so each wave reads its fragments from LDS rather than from L2 -- every wave
+  // loading all of X measured 1.3-1.6x slower at M = 4. Then each wave's X fragments (token
+  // t, lane l: segment l % 16, k-group l / 16, k-step k) go to registers for the whole walk.
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int u = 0; u < KS; ++u)
+        buf_load16_lds(rx, ring + XOFF + t * RB + u * 1024, dv[u] + (uint32_t)t * p.lda_b, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // X before the fills: the waits count in order
+  fill(0);
+  fill(1);
+  // X landed (wave 0's DMA, older than its fills); a bare barrier: __syncthreads() would
+  // also wait for every fill in flight
+  if (wave == 0) __builtin_amdgcn_s_waitcnt(wait_vm_dec(2 * KS));
+  __builtin_amdgcn_s_barrier();
+  i32x4 xr[MT][KS];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      xr[t][k] = t < p.M ? *(const i32x4*)(ring + XOFF + t * RB + fo[k]) : i32x4{0, 0, 0, 0};
+  for (int q = 0; q < nq; ++q) {
+    // row q landed (the KS loads of row q + 1 may still be in flight); lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(wait_vm_dec(KS) & ~(15 << 8));
+    const float add = ra_vec ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bias_l), q)) + e.cadd
+                             : add0;
+    const uint8_t* slot = ring + (2 * wave + (q & 1)) * RB;
+    i32x4 w[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) w[k] = *(const i32x4*)(slot + fo[k]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot is read
+    __builtin_amdgcn_sched_barrier(0);
+    fill(q + 2);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if (t < p.M) {
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[k]),
+                                                      __builtin_bit_cast(bf16x8, xr[t][k]), a, 0, 0, 0);
+        // the trace: lane l holds D[4 (l / 16) + c][l % 16]; the diagonal is component l % 4
+        // of the lanes with (l % 16) / 4 == l / 16 (lanes 0-3, 20-23, 40-43, 60-63)
+        const int sel = lane & 3;
+        float x = diag ? (sel == 0 ? a.x : sel == 1 ? a.y : sel == 2 ? a.z : a.w) : 0.f;
+        x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, false));
+        x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, false));
+        const float v =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 20)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 40)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 60));
+        float o = v * sc + add;
+        if (fused) o = act4(e.act, f32x4{o, 0.f, 0.f, 0.f}).x;
+        res[t] = lane == q ? o : res[t];
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // every fill landed (none lands after the exit)
+  // the stores: lane q holds row q's results
+  if (lane < nq) {
+    const int n = row_of(lane);
+    if (n < p.N) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        if (t < p.M) {
+          const int64_t idx = (int64_t)t * p.ldc + n;
+          const float v = res[t];
+          if (p.c_dt == HKX_BF16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+          else if (p.c_dt == HKX_FP16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_f16x2(v, 0.f) & 0xffffu);
+          else if (p.c_dt == HKX_FP32) ((float*)p.c)[idx] = v;
+          else if (p.c_dt == HKX_FP8E4M3) ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_e4m3(v);
+          else ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_i8(v);
+        }
+      }
+    }
+  }
+}
+
+// Whether the per-wave whole-row kernel takes a call: K = 1024 (M <= 3) or 2048 (M <= 2), the
+// fast epilogue form without a tile operand, 64 or fewer rows a wave (results wait one a
+// lane: N <= 131072 on 256 workgroups), row offsets within 31 bits.
+bool roww_takes(const DecodeArgs& a, int grid) {
+  const bool tile = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
+  const int ks = a.g_total / 4;  // 128-element groups / 4 = K / 512
+  const int nck = (a.N + 7) / 8;
+  return ((ks == 2 && a.M <= 3) || (ks == 4 && a.M <= 2)) && a.g_total % 4 == 0 &&
+         stream_fast(a) && !tile && (nck + grid - 1) / grid <= 64 &&
+         (int64_t)a.N * a.ldb_b < (1LL << 31);
+}
+
+hipError_t launch_roww(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.g_total / 4) {
+    case 2: hipLaunchKernelGGL(roww_kernel<2>, grid, dim3(512), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(roww_kernel<4>, grid, dim3(512), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Whether the whole-row kernel takes a call the stream kernel takes: K = 4096, M <= 4, N up
 // to 32768, the fast epilogue form without a tile operand (every chunk's byte offset then
 // fits 32 bits). At the LM head's N (151936) it measured 1% faster at M = 1 and 3% slower at

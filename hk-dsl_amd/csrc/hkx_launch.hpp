@@ -67,6 +67,10 @@ hipError_t launch_stream(const DecodeArgs& a, dim3 grid, hipStream_t s);
 // the whole-row decode kernel (K = 4096, M <= 4, N <= 32768), for calls stream_takes accepts
 bool rows_takes(const DecodeArgs& a);
 hipError_t launch_rows(const DecodeArgs& a, dim3 grid, hipStream_t s);
+// the per-wave whole-row decode kernel (K = 1024 with M <= 3, K = 2048 with M <= 2), for calls
+// stream_takes accepts; grid: the workgroups it will be launched with
+bool roww_takes(const DecodeArgs& a, int grid);
+hipError_t launch_roww(const DecodeArgs& a, dim3 grid, hipStream_t s);
 
 hipError_t launch_reduce(const ReduceArgs& a, const HkxEpilogue& ep, bool program, dim3 grid,
                          hipStream_t s);

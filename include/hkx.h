@@ -195,9 +195,11 @@ typedef struct HkxEpilogue {
 /* HKX_KERNEL_DECODE variant bits. */
 #define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W (M <= 16, or M <= 32 from K =
                              2048; K a multiple of 1024 up to 32768, no split, unpaired): in
-                             blocks of 16 rows, or, at K = 4096, M <= 4, N <= 32768 with no
-                             residual and no vector scale, in chunks of 4 whole rows strided
-                             over the workgroups; other calls take the blocked kernel */
+                             blocks of 16 rows, or, with no residual and no vector scale, in
+                             chunks of whole rows strided over the workgroups -- 4 rows at
+                             K = 4096, M <= 4, N <= 32768; 8 rows, one a wave, at K = 1024
+                             (M <= 3) and K = 2048 (M <= 2); other calls take the blocked
+                             kernel */
 
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */

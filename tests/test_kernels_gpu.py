@@ -435,6 +435,62 @@ def test_decode_rows_bias_many_groups(m, n):
     assert (c[:, n:].float() == 7.0).all()
 
 
+@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("nk", [(12288, 1024), (49152, 1024), (4100, 2048), (24576, 2048), (1000, 1024),
+                                (8, 2048), (2056, 1024)])
+def test_decode_per_wave_rows(m, nk):
+    """The per-wave whole-row decode kernel (K = 1024 with M <= 3, K = 2048 with M <= 2; the
+    stream kernel above): bias, rows a wave from 1 to 24 (49152 rows), ragged N (rows past N
+    read zero and are never written), a W of row stride K + 64, an output of row stride
+    N + 8 with sentinels."""
+    n, k = nk
+    a, b = _data(m, n, k, seed=38)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(39)).to(torch.bfloat16)
+    ref = O.apply_epilogue("bias", O.gemm_fp32(a, b), bias=bias)
+    wide = torch.zeros(n, k + 64, dtype=b.dtype)
+    wide[:, :k] = b
+    c = torch.full((m, n + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+    _run(a.to(DEV), wide.to(DEV)[:, :k], c[:, :n], kernel=nat.KERNEL_DECODE,
+         variant=nat.DEC_STREAM, ep=_fused([(bias.to(DEV), nat.ROW)], ra=0))
+    O.assert_close(c[:, :n], ref, rtol=1e-2, atol=1e-2)
+    assert (c[:, n:].float() == 7.0).all()
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16, torch.float32, torch.int8,
+                                 torch.float8_e4m3fn], ids=["bf16", "fp16", "fp32", "int8", "fp8"])
+def test_decode_per_wave_rows_forms(odt):
+    """The per-wave kernel's epilogue and stores: none; a broadcast per-token scale with cmul,
+    a bias, cadd and GELU; and the 8-bit stores (int8 within one quantizer step of the
+    oracle's, fp8 e4m3 saturating at 448)."""
+    m, n, k = 2, 3000, 2048
+    a, b = _data(m, n, k, seed=40)
+    acc = O.gemm_fp32(a, b)
+    ad, bdev = a.to(DEV), b.to(DEV)
+    if odt in (torch.int8, torch.float8_e4m3fn):
+        mul = 40.0 if odt == torch.int8 else 300.0
+        c = torch.empty((m, n), dtype=odt, device=DEV)
+        _run(ad, bdev, c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM, ep=_fused([], cmul=mul))
+        if odt == torch.int8:
+            assert (c.cpu().float() - O.quantize_int8(acc * mul)).abs().max().item() <= 1.0
+        else:
+            want = (acc * mul).clamp(-448, 448)
+            got = c.cpu().float()
+            big = want.abs() > 16
+            assert ((got - want).abs() / want.abs())[big].max().item() < 0.07
+            assert got.abs().max().item() == 448.0
+        return
+    c = torch.empty((m, n), dtype=odt, device=DEV)
+    _run(ad, bdev, c, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM)
+    O.assert_close(c, acc, rtol=1e-2, atol=1e-2)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(41)).to(torch.bfloat16)
+    sd = torch.full((1, 1), 0.75, device=DEV).expand(m, 1)
+    ep = _fused([(sd, nat.COL), (bias.to(DEV), nat.ROW)], cs=0, ra=1, act=nat.ACT_GELU_TANH,
+                cmul=0.5, cadd=0.25)
+    c2 = torch.empty((m, n), dtype=odt, device=DEV)
+    _run(ad, bdev, c2, kernel=nat.KERNEL_DECODE, variant=nat.DEC_STREAM, ep=ep)
+    O.assert_close(c2, O.gelu_tanh(acc * 0.375 + bias.float() + 0.25), rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("m", [1, 3, 7, 16])
 @pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16, torch.float32],
                          ids=["bf16", "fp16", "fp32"])
