@@ -356,13 +356,14 @@ def ref_table():
 
 
 ARMS = ["cfg2_bias_gelu", "cfg2_plain", "cfg2_hipblaslt", "cfg2_bias_gelu_zero_x",
-        "cfg5_deq_bias", "cfg5_deq_bias_zero_x", "cfg5_torch_scaled_mm"]
+        "cfg5_deq_bias", "cfg5_deq_bias_zero_x", "cfg5_torch_scaled_mm", "cfg2_plain_4wave"]
 
 
 def arms():
     """The workload of the clock-and-cycles profile: config 2 (bias + GELU, plain, hipBLASLt's
-    plain GEMM through torch.matmul, bias + GELU on an all-zero x) and config 5 (dequant +
-    bias, the same on an all-zero x, torch._scaled_mm), each 0.4 s of untimed calls, a
+    plain GEMM through torch.matmul, bias + GELU on an all-zero x), config 5 (dequant +
+    bias, the same on an all-zero x, torch._scaled_mm) and config 2's plain GEMM on the
+    4-wave kernel (one wave a SIMD, 128 x 128 a wave), each 0.4 s of untimed calls, a
     50 ms pause, 30 calls, a 50 ms pause -- so a trace splits into the arms by its gaps. Run
     under rocprofv3 twice: --kernel-trace, and --pmc GRBM_GUI_ACTIVE ...; then
     `bench.py --arms-summary TRACE_DIR PMC_DIR` prints the table."""
@@ -393,7 +394,8 @@ def arms():
            lambda: sm(x8, w8, sa, sb, bias=b5, out=y5),
            lambda: sm(z8, w8, sa, sb, bias=b5, out=y5),
            lambda: torch._scaled_mm(x8, w8.t(), scale_a=sa, scale_b=sb.reshape(1, -1),
-                                    out_dtype=torch.bfloat16)]
+                                    out_dtype=torch.bfloat16),
+           lambda: T(x, w, out=y, schedule="t256w4")]
     for name, fn in zip(ARMS, fns):
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < 0.4:
@@ -417,7 +419,7 @@ def arms_summary(trace_dir, pmc_dir):
     import csv
 
     def gemm(name):
-        return "quad" in name or "Cijk" in name
+        return "quad" in name or "Cijk" in name or "tile4" in name
 
     def by_gap(items, st, en):
         out, last = [], None
@@ -451,6 +453,15 @@ def arms_summary(trace_dir, pmc_dir):
         f, pk = flops[name[:4]], peak[name[:4]]
         print(f"| {name} | `{kn}` | {us:.1f} | {cyc / 1e3:.0f} K | {cyc / us / 1e3:.2f} | "
               f"{f / (us * 1e-6) / pk:.3f} | {f / (cyc / 2.4e9) / pk:.3f} |")
+    # every other counter of the run: median over the timed calls, millions, summed over the chip
+    names = sorted({k for a in carms for c in a for k in c["c"]} - {"GRBM_GUI_ACTIVE"})
+    if names:
+        print()
+        print("| arm | " + " | ".join(names) + " |")
+        print("|---|" + "---:|" * len(names))
+        for name, ca in zip(ARMS, carms):
+            vals = [statistics.median(c["c"][k] for c in ca[-30:]) / 1e6 for k in names]
+            print(f"| {name} | " + " | ".join(f"{v:.2f}" for v in vals) + " |")
 
 
 def main():
