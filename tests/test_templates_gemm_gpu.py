@@ -222,10 +222,8 @@ def test_config2_bias_gelu_full_size():
     got = T(xd, wd, epilogue=T.bias_gelu, bias=bd)
     ref = O.gelu_tanh(xd.float() @ wd.float().t() + bd.float())  # fp32 reference on the GPU
     torch.testing.assert_close(got.float(), ref, rtol=1e-2, atol=1e-2)
-    # and the CPU oracle on 64-row slices in the first, a middle and the last 256-row tile
-    for r0 in (0, 2000, 4096 - 64):
-        rows = slice(r0, r0 + 64)
-        O.assert_close(got[rows], O.linear_bias_gelu(x[rows], w, b), rtol=1e-2, atol=1e-2)
+    # and the CPU oracle on the whole output (fp32 on the host's cores, about a second)
+    O.assert_close(got, O.linear_bias_gelu(x, w, b), rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("m", [2048, 8192])
@@ -236,12 +234,9 @@ def test_config3_gate_up_silu_and_mul(m):
     acc = xd.float() @ wd.float().t()
     ref = O.silu_and_mul(acc[:, :12288], acc[:, 12288:])
     torch.testing.assert_close(got.float(), ref, rtol=1e-2, atol=1e-2)
-    # and the CPU oracle on 32-row slices in the first, a middle and the last 256-row tile
-    wt = w.t().contiguous()
-    for r0 in (0, m // 2 + 100, m - 32):
-        rows = slice(r0, r0 + 32)
-        a = O.gemm_fp32(x[rows], wt)
-        O.assert_close(got[rows], O.silu_and_mul(a[:, :12288], a[:, 12288:]), rtol=1e-2, atol=1e-2)
+    # and the CPU oracle on the whole output
+    a = O.gemm_fp32(x, w.t().contiguous())
+    O.assert_close(got, O.silu_and_mul(a[:, :12288], a[:, 12288:]), rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("m", [1, 4, 16])
@@ -277,11 +272,9 @@ def test_config5_fp8_scaled_dequant():
     got0 = hk.ops.scaled_mm(xd, bd8, sa.to(DEV), sb.to(DEV))
     ref0 = (xd.float() @ bd8.float().t()) * sa.to(DEV) * sb.to(DEV)
     assert O.rel_to_max(got0, ref0) < 8e-3
-    # and the CPU oracle on 32-row slices in the first, a middle and the last 256-row tile
-    for r0 in (0, 4100, m - 32):
-        rows = slice(r0, r0 + 32)
-        O.assert_close(got[rows], O.scaled_mm(x8[rows], b8, sa[rows], sb, bias), rtol=3e-2, atol=1e-2)
-        assert O.rel_to_max(got0[rows].cpu(), O.scaled_mm(x8[rows], b8, sa[rows], sb)) < 8e-3
+    # and the CPU oracle on the whole output, with and without the bias
+    O.assert_close(got, O.scaled_mm(x8, b8, sa, sb, bias), rtol=3e-2, atol=1e-2)
+    assert O.rel_to_max(got0.cpu(), O.scaled_mm(x8, b8, sa, sb)) < 8e-3
 
 
 def test_scaled_mm_per_tensor_and_ragged_m():
