@@ -17,8 +17,8 @@
 //   of row l % 32 / 4's line, so every request is a whole line, and the 64-byte K-halves
 //   keep the bank pattern of 64-byte rows (16-byte chunk c of row r at c ^ swz4(r)).
 // * Phases. Per K-tile t, two phases, each: LDS reads into registers, fills, a barrier,
-//   the MFMAs of two blocks (32 v_mfma_f32_16x16x32_bf16, or 8 fp8 32 x 32 x 64), a
-//   barrier:
+//   the MFMAs of two blocks (32 v_mfma_f32_16x16x32_bf16, 16 fp8 16 x 16 x 128, or 8 MX
+//   32 x 32 x 64), a barrier:
 //     1: read A0(t), B0(t);      fill A1(t + 1), B1(t + 2);   math (0, 0), (0, 1)
 //     2: read A1(t), B1(t + 1);  fill B0, A0 of t + 2;         math (1, 0), (1, 1)
 //   (the MX form reads B1(t) in phase 1 and fills B1(t + 2) in phase 2 with B0 and A0).
@@ -74,6 +74,15 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                     : (EPF == kEpNone || EPF == kEpBias || EPF == kEpTile), "forms");
   static_assert(!PAIR || (!FP8 && EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
   static_assert(SMEM <= 160 * 1024, "LDS");
+
+  // Fragment layout: W32, the MX form, 32 x 32 x 64 scaled MFMAs (its E8M0 block scales
+  // follow that instruction's K blocks); every other form 16 x 16 fragments -- bf16
+  // 16 x 16 x 32, plain fp8 16 x 16 x 128 (the K-tile's 128 bytes in one MFMA). The fp8
+  // 16 x 16 x 128 MFMA runs 9% more flops than 32 x 32 x 64 on random operands under the
+  // board's power limit (4.34 against 3.97 PFLOP/s, a register-only loop on one box), for
+  // the same operand registers, accumulators and LDS reads a K-tile.
+  constexpr bool W32 = MX;
+  constexpr int KH = FP8 && !MX ? 1 : 2;  // MFMA K-steps a fragment a K-tile
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
@@ -214,7 +223,7 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   // and 16-31 as block 1, so lane half h holds K [16 h, +16) of each 32-K block; at
   // r0 * 128 + s * 512 + rdo[0 or 1].
   uint32_t rdo[2];
-  if constexpr (FP8) {
+  if constexpr (W32) {
     const int rf = lane & 31, h = lane >> 5;
     const int sw = ((rf >> 4) & 1) | (((rf >> 3) & 1) << 1);
 #pragma unroll
@@ -226,14 +235,21 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     for (int par = 0; par < 2; ++par)
       rdo[par] = (uint32_t)((rr >> 3) * 1024 + (rr & 7) * 64 + ((q ^ (par | ((rr >> 3) << 1))) << 4));
   }
-  constexpr int NA = FP8 ? 2 : 4, NB = FP8 ? 1 : 2;  // fragments of a block's A and B rows
+  constexpr int NA = W32 ? 2 : 4, NB = W32 ? 1 : 2;  // fragments of a block's A and B rows
   using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
   // [fragment][K-half]; bfn: B1 of the next K-tile (see the K loop)
   Frag af[NA][2], bf0[NB][2], bf1[NB][2], bfn[NB][2];
   auto frag_at = [&](const uint8_t* s, int r0, int h, int par) -> Frag {
-    if constexpr (FP8) {
+    if constexpr (W32) {
       const i32x4 lo = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[0]);
       const i32x4 hi = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[1]);
+      return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    } else if constexpr (FP8) {
+      // 16 x 16 x 128: the bf16 fragment's 16-byte chunk of both K-halves, so lane l holds
+      // K 16 (l / 16) + [0, 16) and 64 + 16 (l / 16) + [0, 16) of row l % 16 -- in A and B
+      // alike, which is all a dot product needs of the K order
+      const i32x4 lo = *(const i32x4*)(s + r0 * 128 + rdo[par]);
+      const i32x4 hi = *(const i32x4*)(s + r0 * 128 + 512 + rdo[par]);
       return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     } else {
       return *(const bf16x8*)(s + r0 * 128 + h * 512 + rdo[par]);
@@ -244,14 +260,14 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
     for (int f = 0; f < NA; ++f)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) af[f][h] = frag_at(s, grp * 64 + (64 / NA) * f, h, f & 1);
+      for (int h = 0; h < KH; ++h) af[f][h] = frag_at(s, grp * 64 + (64 / NA) * f, h, f & 1);
   };
   auto read_b = [&](int slot, int j, Frag (&bf)[NB][2]) {
     const uint8_t* s = quarter(slot, 2 + j);
 #pragma unroll
     for (int g = 0; g < NB; ++g)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) bf[g][h] = frag_at(s, wc * 32 + 16 * g, h, g & 1);
+      for (int h = 0; h < KH; ++h) bf[g][h] = frag_at(s, wc * 32 + 16 * g, h, g & 1);
   };
 
   // MX: the E8M0 dword of each of this lane's fragment rows for the K-tile (its 4 blocks,
@@ -273,12 +289,12 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     }
   };
 
-  using Acc = typename std::conditional<FP8, f32x16, f32x4>::type;
+  using Acc = typename std::conditional<W32, f32x16, f32x4>::type;
   Acc acc[NI][2][NA][NB];  // [A half][B half][row fragment][column fragment]
   auto math = [&](int i, int j, const Frag (&bf)[NB][2], bool zero) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < KH; ++h)
 #pragma unroll
       for (int f = 0; f < NA; ++f)
 #pragma unroll
@@ -293,8 +309,8 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                   bf[g][h], af[f][h], c, 0, 0, 2, (int)scb[j], 2, (int)sca[i][f]);
           }
           else if constexpr (FP8)
-            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
-                                                                              0, 0, 0);
+            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
+                                                                               0, 0, 0);
           else
             acc[i][j][f][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[g][h], af[f][h], c, 0, 0, 0);
         }
@@ -317,9 +333,8 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     tile_at(lt, m0, n0);
     const uint8_t* ev = smem + EPV + (lt % 3) * 3072;  // cs, rs, ra
     if constexpr (SHARE) {
-      // the split's fp32 sums, 16 bytes a lane: bf16 (16 x 16 fragments) lane (rf, q) holds
-      // row rf, columns 4 q + [0, 4) of each fragment; fp8 (32 x 32) lane (rf, h) holds row
-      // rf, columns 8 g + 4 h + [0, 4) of run g
+      // the split's fp32 sums, 16 bytes a lane (16 x 16 fragments; the split form is never
+      // MX): lane (rf, q) holds row rf, columns 4 q + [0, 4) of each fragment
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -329,52 +344,22 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
             for (int g = 0; g < NB; ++g) {
               __builtin_amdgcn_sched_barrier(0);
-              if constexpr (FP8) {
-                const int ml = 128 * i + 64 * grp + 32 * f + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                  const int n = n0 + 128 * j + 32 * wc + 8 * r + 4 * (lane >> 5);
-                  const Acc& a = acc[i][j][f][g];
-                  store_c(__builtin_bit_cast(i32x4, f32x4{a[4 * r], a[4 * r + 1], a[4 * r + 2], a[4 * r + 3]}),
-                          n < p.N, (uint32_t)(m0 + ml) * row_b + (uint32_t)n * 4u);
-                }
-              } else {
-                const int ml = 128 * i + 64 * grp + 16 * f + (lane & 15);
-                const int n = n0 + 128 * j + 32 * wc + 16 * g + 4 * (lane >> 4);
-                store_c(__builtin_bit_cast(i32x4, acc[i][j][f][g]), n < p.N,
-                        (uint32_t)(m0 + ml) * row_b + (uint32_t)n * 4u);
-              }
+              const int ml = 128 * i + 64 * grp + 16 * f + (lane & 15);
+              const int n = n0 + 128 * j + 32 * wc + 16 * g + 4 * (lane >> 4);
+              store_c(__builtin_bit_cast(i32x4, acc[i][j][f][g]), n < p.N,
+                      (uint32_t)(m0 + ml) * row_b + (uint32_t)n * 4u);
             }
       return;
     }
-    if constexpr (FP8) {
-      // 32 x 32: lane l (row l % 32, half h = l / 32) holds columns 8 g + 4 h + [0, 4) in
-      // run g of a fragment's 16 values; runs 2 t and 2 t + 1 trade halves
-      // (v_permlane32_swap), so lane l stores columns 16 t + 8 h + [0, 8)
-      const int rf = lane & 31, h = lane >> 5;
-      // the row scales of this lane's four rows, read once; a column run's scales and bias
-      // are read once for the four row fragments that share them (one LDS wait a run,
-      // where a wait before every store left the epilogue on LDS latency)
-      [[maybe_unused]] float cs[2][2];
-      if constexpr (deq) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int f = 0; f < 2; ++f) cs[i][f] = cs_bc ? cs0 : ((const float*)ev)[128 * i + 64 * grp + 32 * f + rf];
-      }
+    if constexpr (W32) {
+      // MX, 32 x 32 (no epilogue operands): lane l (row l % 32, half h = l / 32) holds
+      // columns 8 g + 4 h + [0, 4) in run g of a fragment's 16 values; runs 2 t and 2 t + 1
+      // trade halves (v_permlane32_swap), so lane l stores columns 16 t + 8 h + [0, 8)
+      const int h = lane >> 5;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         __builtin_amdgcn_sched_barrier(0);
         const int cb = 128 * j + 32 * wc;  // the block's first column
-        [[maybe_unused]] f32x4 rs[2][2], bv[2][2];  // [run t][u]
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int col = cb + 16 * t + 8 * u + 4 * h;
-            if constexpr (deq) rs[t][u] = rs_bc ? f32x4{rs0, rs0, rs0, rs0} : *(const f32x4*)(ev + 1024 + col * 4);
-            if constexpr (bias) bv[t][u] = unpack_bf16x4(*(const u32x2*)(ev + 2048 + col * 2));
-          }
         // after the 16-lane trade below, lane l stores row 16 s + l % 16 of the fragment
         // (s: which of the two registers), columns 16 ((l >> 4) & 1) + 8 (l >> 5) + [0, 8)
         // of the block: each store covers 16 rows x 64 contiguous bytes (four lanes a row),
@@ -394,8 +379,6 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                 const Acc& a = acc[i][j][f][0];
                 const int r = 8 * t + 4 * u;
                 v[u] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
-                if constexpr (deq) v[u] = v[u] * (rs[t][u] * cs[i][f]);
-                if constexpr (bias) v[u] += bv[t][u];
               }
               const u32x2 w0 = pack4<2>(HKX_BF16, v[0]), w1 = pack4<2>(HKX_BF16, v[1]);
               uint32_t x0 = w0.x, x1 = w1.x, y0 = w0.y, y1 = w1.y;
@@ -419,6 +402,23 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
       }
     } else {
     const int rf = lane & 15, q = lane >> 4;
+    // fp8 dequant: this lane's row scales [i][f] (row 128 i + 64 grp + 16 f + rf) and the
+    // column scales of its columns [j][g] (as the bias), read once a tile
+    [[maybe_unused]] float rsc[NI][4];
+    [[maybe_unused]] f32x4 csc[2][2];
+    if constexpr (deq) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) rsc[i][f] = cs_bc ? cs0 : ((const float*)ev)[128 * i + 64 * grp + 16 * f + rf];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const int col = 128 * j + 32 * wc + 16 * g + 4 * q;
+          csc[j][g] = rs_bc ? f32x4{rs0, rs0, rs0, rs0} : *(const f32x4*)(ev + 1024 + col * 4);
+        }
+    }
     [[maybe_unused]] f32x4 bv[2][2];
     if constexpr (bias) {
       const uint32_t* bs = (const uint32_t*)(ev + 2048);
@@ -488,6 +488,10 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
         for (int f = 0; f < 4; ++f) {
           __builtin_amdgcn_sched_barrier(0);
           f32x4 va = acc[i][j][f][0], vb = acc[i][j][f][1];
+          if constexpr (deq) {
+            va = va * (csc[j][0] * rsc[i][f]);
+            vb = vb * (csc[j][1] * rsc[i][f]);
+          }
           if constexpr (bias) {
             va += bv[j][0];
             vb += bv[j][1];
