@@ -595,10 +595,11 @@ def measured_peaks():
             "mfma_fp8_random_operands_tflops": round(peaks.mfma_random_tflops(True), 1),
             "hbm_read_gbs": round(hbm, 1),
             "hbm_read_gbs_by_kernel": {k: round(v, 1) for k, v in hbm_by.items()},
-            "how": "hk.peaks: register-only 32x32 MFMA loop on every CU, on constant operands "
+            "how": "hk.peaks: register-only MFMA loops on every CU, 32x32 on constant operands, "
                    "and on random ones (the power-limited rate on data that toggles like real "
-                   "tensors); HBM: four 1 GiB buffers read in rotation past the 256 MB "
-                   "Infinity Cache, the best of three read kernels"}
+                   "tensors) the better of the 32x32 and 16x16 instructions; HBM: four 1 GiB "
+                   "buffers read in rotation past the 256 MB Infinity Cache, the best of three "
+                   "read kernels"}
 
 
 def other_configs(steps, warmup, peaks):

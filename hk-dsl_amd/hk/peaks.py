@@ -21,7 +21,7 @@ def _lib():
         if not path.is_file():
             raise RuntimeError(f"{path} is not built; run hk-dsl_amd/build.py")
         _LIB = ctypes.CDLL(str(path))
-        for f in ("hkxp_mfma", "hkxp_mfma_rand", "hkxp_mfma_issue", "hkxp_read", "hkxp_read_v",
+        for f in ("hkxp_mfma", "hkxp_mfma_rand", "hkxp_mfma_rand16", "hkxp_mfma_issue", "hkxp_read", "hkxp_read_v",
                   "hkxp_clock", "hkxp_lds"):
             getattr(_LIB, f).restype = ctypes.c_int
     return _LIB
@@ -67,23 +67,34 @@ def mfma_tflops(fp8: bool = False, device="cuda:0") -> float:
     return blocks * 4 * iters * 4 * flops_per / t / 1e12
 
 
-def mfma_random_tflops(fp8: bool = False, device="cuda:0") -> float:
-    """mfma_tflops's loop on random operands (random sign and mantissa bits, four operand
-    sets rotated): the MFMA rate when the datapath toggles as on real tensors. Under the
-    board's power limit this runs at a lower clock than the constant-operand loop, so it is
-    the ceiling a GEMM on random data can reach with its MFMAs busy every cycle."""
+def mfma_random_tflops(fp8: bool = False, device="cuda:0", shape: str = "best") -> float:
+    """An MFMA loop on random operands (random sign and mantissa bits, four operand sets
+    rotated): the MFMA rate when the datapath toggles as on real tensors. Under the board's
+    power limit this runs at a lower clock than the constant-operand loop, so it is the
+    ceiling a GEMM on random data can reach with its MFMAs busy every cycle. `shape` "32"
+    times the 32 x 32 instructions (v_mfma_f32_32x32x16_bf16, v_mfma_scale_f32_32x32x64_f8f6f4),
+    "16" the 16 x 16 ones the GEMM kernels issue (16x16x32 bf16, 16x16x128 fp8), "best" the
+    higher of the two."""
     import torch  # noqa: PLC0415
 
+    if shape == "best":
+        return max(mfma_random_tflops(fp8, device, "16"), mfma_random_tflops(fp8, device, "32"))
     L = _lib()
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     blocks, iters = cus * 8, 1000
     out = torch.zeros(blocks, device=device)
     st = torch.cuda.current_stream(device).cuda_stream
-    t = _time(lambda: L.hkxp_mfma_rand(int(fp8), blocks, iters, ctypes.c_void_p(out.data_ptr()),
-                                       ctypes.c_void_p(st)), warm_s=0.5)
-    flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
-    # 4 waves a workgroup, 16 MFMAs a wave an iteration (4 operand sets x 4 accumulators)
-    return blocks * 4 * iters * 16 * flops_per / t / 1e12
+    fn = L.hkxp_mfma_rand16 if shape == "16" else L.hkxp_mfma_rand
+    t = _time(lambda: fn(int(fp8), blocks, iters, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)),
+              warm_s=0.5)
+    if shape == "16":
+        flops_per = 2 * 16 * 16 * (128 if fp8 else 32)
+        per_wave = 32  # 4 operand sets x 8 accumulators
+    else:
+        flops_per = 2 * 32 * 32 * (64 if fp8 else 16)
+        per_wave = 16  # 4 operand sets x 4 accumulators
+    # 4 waves a workgroup
+    return blocks * 4 * iters * per_wave * flops_per / t / 1e12
 
 
 def mfma_issue_tflops(waves_per_simd: int = 1, device="cuda:0") -> float:

@@ -7,9 +7,11 @@
 //   hkxp_clock(out, iters, stream)                -> shader clock ticks vs the 100 MHz
 //                                                    real-time counter, under MFMA load
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -46,9 +48,14 @@ __device__ inline uint32_t mix32(uint32_t x) {
   x ^= x >> 16; x *= 0x7feb352dU; x ^= x >> 15; x *= 0x846ca68bU; x ^= x >> 16;
   return x;
 }
-template <bool FP8, int CH = 4>
+// W16: the 16 x 16 instructions the GEMM kernels issue (v_mfma_f32_16x16x32_bf16,
+// v_mfma_scale_f32_16x16x128_f8f6f4), 8 accumulators a wave; else the 32 x 32 ones, 4. On
+// random operands the 16 x 16 forms run the more flops under the power limit (bf16 about 3%,
+// fp8 about 9%), so they set the ceiling.
+template <bool FP8, bool W16 = false, int CH = W16 ? 8 : 4>
 __global__ void __launch_bounds__(256) mfma_rand_loop(float* out, int iters) {
-  f32x16 acc[CH] = {};
+  using Acc = typename std::conditional<W16, f32x4, f32x16>::type;
+  Acc acc[CH] = {};
   const uint32_t seed = (uint32_t)(blockIdx.x * 256 + threadIdx.x) * 0x9E3779B9u;
   i32x4 ab[8];   // bf16: 4 A and 4 B operand sets
   i32x8 fb[8];   // fp8
@@ -68,9 +75,16 @@ __global__ void __launch_bounds__(256) mfma_rand_loop(float* out, int iters) {
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        if constexpr (FP8)
+        if constexpr (FP8 && W16)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fb[u], fb[4 + ((u + j) & 3)], acc[j], 0, 0, 0,
+                                                                    0, 0, 0);
+        else if constexpr (FP8)
           acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[u], fb[4 + ((u + j) & 3)], acc[j], 0, 0, 0,
                                                                    0, 0, 0);
+        else if constexpr (W16)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ab[u]),
+                                                           __builtin_bit_cast(bf16x8, ab[4 + ((u + j) & 3)]),
+                                                           acc[j], 0, 0, 0);
         else
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ab[u]),
                                                            __builtin_bit_cast(bf16x8, ab[4 + ((u + j) & 3)]),
@@ -79,7 +93,7 @@ __global__ void __launch_bounds__(256) mfma_rand_loop(float* out, int iters) {
   }
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < CH; ++j) s += acc[j][0] + acc[j][15];
+  for (int j = 0; j < CH; ++j) s += acc[j][0] + acc[j][3];
   if (s == 1234.5f) out[blockIdx.x] = s;
 }
 
@@ -224,6 +238,14 @@ int hkxp_mfma_rand(int fp8, int blocks, int iters, float* out, void* stream) {
     hipLaunchKernelGGL(mfma_rand_loop<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
   else
     hipLaunchKernelGGL(mfma_rand_loop<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return (int)hipGetLastError();
+}
+
+int hkxp_mfma_rand16(int fp8, int blocks, int iters, float* out, void* stream) {
+  if (fp8)
+    hipLaunchKernelGGL((mfma_rand_loop<true, true>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  else
+    hipLaunchKernelGGL((mfma_rand_loop<false, true>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
   return (int)hipGetLastError();
 }
 
