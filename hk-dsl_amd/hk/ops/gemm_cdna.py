@@ -136,7 +136,14 @@ def rule(m: int, n: int, k: int, fp8: bool = False) -> str:
     split over K in powers of two while the workgroups stay within the CUs and each split
     keeps 16 or more 128-byte K units. On the shipped table's 132 measured points its pick
     is 2% slower than the best candidate on average (the rule before the 128-column tiles:
-    26%)."""
+    26%).
+
+    fp8 has no measured table, so its last step follows one measured sweep (scaled_mm with
+    dequant and bias, N x K in {4096 x 4096, 12288 x 4096, 4096 x 12288}, M 256-4096, every
+    tile candidate, M 16-4096): from M = 129 to 512, 64 x 128 tiles, split only where each
+    split keeps 32 K units (4096 x 4096 at M = 256: 12.1-12.2 us on 64 x 128 tiles against
+    19.6 on 128 x 128 ones split in two; at M = 512 13.9 against 21.9; 4096 x 12288 at M =
+    256 split in two, 23.9 against 29.9 unsplit); up to M = 128 the bf16 steps."""
     if not fp8 and m <= 32 and k % 128 == 0:
         return "decode"
     kunits = k * (1 if fp8 else 2) // 128
@@ -150,11 +157,12 @@ def rule(m: int, n: int, k: int, fp8: bool = False) -> str:
         return "q128" if not fp8 and kunits <= 64 else "t128"
     if m > 64 and tiles(128, 128) >= 0.75 * CUS:
         return "t128x128"
-    bm = 64 if m <= 128 else 128
+    bm = 64 if m <= (512 if fp8 else 128) else 128
     t = tiles(bm, 128)
     most = 8 if bm == 64 else 4  # the split candidates there are
+    per_split = 32 if fp8 and m > 128 else 16  # K units a split keeps at least
     splits = 1
-    while t * splits * 2 <= CUS and kunits // (splits * 2) >= 16 and splits < most:
+    while t * splits * 2 <= CUS and kunits // (splits * 2) >= per_split and splits < most:
         splits *= 2
     return f"t{bm}x128" + (f"k{splits}" if splits > 1 else "")
 
