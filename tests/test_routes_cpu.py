@@ -174,3 +174,25 @@ def test_rule_close_to_the_measured_best():
         ratios.append(us["hk:" + pick] / best)
     assert sum(ratios) / len(ratios) < 1.05
     assert max(ratios) < 1.5
+
+
+def test_fp8_rule_follows_its_sweep(monkeypatch):
+    """The fp8 rule's picks at the sweep's points where it chose the measured best
+    (scaled_mm with dequant + bias; fp8 has no measured table): 64 x 128 tiles from M = 129
+    to 512, a split over K only where each split keeps 32 K units, the bf16 steps below."""
+    monkeypatch.setattr(gemm_cdna, "OVERRIDE", {})
+    want = {
+        (256, 4096, 4096): "t64x128",        # 12.1-12.2 us; split on 128 x 128: 19.6
+        (512, 4096, 4096): "t64x128",        # 13.9; the former pick 21.9
+        (256, 4096, 12288): "t64x128k2",     # 23.9; unsplit 29.9
+        (512, 4096, 12288): "t64x128",       # 32.4
+        (1024, 4096, 4096): "t128x128",      # 22.3
+        (2048, 4096, 4096): "t128",          # 37.2
+        (256, 12288, 4096): "t128x128",      # 20.3-20.5
+        (1024, 12288, 4096): "t256",         # 42.1
+        (4096, 4096, 12288): "t256",         # 133.0
+        (128, 4096, 12288): "t64x128k4",     # 18.3
+    }
+    for (m, n, k), name in want.items():
+        assert gemm_cdna.route(m, n, k, fp8=True) == name, (m, n, k)
+        assert gemm_cdna.fits(name, m, n, k, fp8=True)
