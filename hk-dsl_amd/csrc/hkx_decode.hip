@@ -296,6 +296,137 @@ __global__ void __launch_bounds__(512) rows_kernel(const DecodeArgs p) {
   __builtin_amdgcn_s_waitcnt(wait_vm_dec(0));  // no fill lands in LDS after the exit
 }
 
+// The whole-row decode GEMM in short workgroups: the rows kernel's chunks, MFMA form and
+// epilogue, but each workgroup takes CPW consecutive chunks (CPW x 32 KB of W, contiguous)
+// and ends, so the grid is N / (4 CPW) workgroups, two (CPW = 2) or four (CPW = 1) resident
+// on a CU at once, and the dispatcher hands a CU its next workgroup when one ends: the
+// chunks even out over a CU's lifetime instead of being fixed at launch. All of a
+// workgroup's fills are issued at its start (X, then on wave 0 the bias values, then the
+// chunks in order), chunk j is multiplied once its fills land, and wave 0 sums the waves'
+// quad sums, applies the epilogue and stores after the last.
+template <int CPW>
+__global__ void __launch_bounds__(512) rowsq_kernel(const DecodeArgs p) {
+  constexpr int NW = 8;
+  constexpr int CH = 32768;  // a chunk: 4 rows x 8 KB
+  constexpr int RED = CPW * CH;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RED + NW * CPW * 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nck = (p.N + 3) / 4;
+  const int c0 = blockIdx.x * CPW;  // this workgroup's first chunk
+  if (c0 >= nck) return;
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.b, p.b_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, p.a_bytes);
+  uint32_t fv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wave >> 1, P = (wave & 1) * 256 + i * 64 + lane;
+    fv[i] = (uint32_t)r * p.ldb_b + (uint32_t)((P ^ (4 * r + (P >> 7))) << 4);
+  }
+  // chunks past N (the last workgroup's second) are filled out of range: they read zeros
+  // and are never stored, and every wave issues the same loads
+  auto fill = [&](int j) {
+    const uint32_t base = c0 + j < nck ? (uint32_t)(c0 + j) * 4u * p.ldb_b : 0x80000000u;
+    uint8_t* slot = ring + j * CH + (wave >> 1) * 8192 + (wave & 1) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf_load16_lds<kNonTemporal>(rw, slot + i * 1024, fv[i] + base, 0);
+  };
+
+  const Fused& e = p.ep;
+  const bool fused = e.form == HKX_EP_FUSED;
+  const bool ra_vec = fused && e.ra.p && e.ra.ld;
+  const float cs_sc = (fused && e.cs.p) ? ld1(e.cs.p, e.cs.dt, 0) * e.cmul : (fused ? e.cmul : 1.0f);
+  const float rs_sc = (fused && e.rs.p) ? ld1(e.rs.p, e.rs.dt, 0) : 1.0f;
+  const float ra_sc = (fused && e.ra.p && !e.ra.ld) ? ld1(e.ra.p, e.ra.dt, 0) : 0.0f;
+  const float sc = cs_sc * rs_sc;
+  const float add0 = ra_sc + e.cadd;
+
+  // X, as the rows kernel holds it: lane l token (l % 16) / 4, quarter l % 4, k-steps
+  // 4 w .. 4 w + 3 of each quarter
+  i32x4 xr[4];
+  {
+    const int tl = (lane & 15) >> 2, sq = lane & 3, kq = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      xr[t] = buf_load16(rx, (uint32_t)tl * p.lda_b + sq * 2048 + (4 * wave + t) * 64 + kq * 16, 0);
+  }
+  // wave 0, lane l: the bias of chunk l / 16's row (l / 4) % 4 (bf16, unit stride)
+  const int fc = lane >> 4, fr = (lane >> 2) & 3, ftl = lane & 3;
+  const int fn = 4 * (c0 + fc) + fr;
+  const bool f_ok = fc < CPW && c0 + fc < nck && fn < p.N;
+  // (one buffer load on every lane of every wave, out of range where unused: a load under
+  // a branch gets a wait of its own at the branch's end, before the fills)
+  const uint16_t bias_w = __builtin_amdgcn_raw_buffer_load_b16(
+      make_rsrc(ra_vec ? e.ra.p : nullptr, ra_vec ? (uint32_t)p.N * 2u : 0u),
+      f_ok && wave == 0 ? (uint32_t)fn * 2u : 0x7ffffff0u, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) fill(j);
+
+  uint32_t wa[4];
+  {
+    const int r = (lane & 15) >> 2, sq = lane & 3, kq = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int gp = 128 * sq + 4 * (4 * wave + t) + kq;
+      wa[t] = (uint32_t)(r * 8192 + ((gp ^ (4 * r + sq)) << 4));
+    }
+  }
+  f32x4 acc[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    // chunk j's fills landed in every wave (the newer chunks' 4 a wave may still run)
+    if (j == CPW - 1) __builtin_amdgcn_s_waitcnt(wait_vm_dec(0) & ~(15 << 8));
+    else if (CPW - 1 - j == 1) __builtin_amdgcn_s_waitcnt(wait_vm_dec(4) & ~(15 << 8));
+    else if (CPW - 1 - j == 2) __builtin_amdgcn_s_waitcnt(wait_vm_dec(8) & ~(15 << 8));
+    else __builtin_amdgcn_s_waitcnt(wait_vm_dec(12) & ~(15 << 8));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* slot = ring + j * CH;
+    i32x4 w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t] = *(const i32x4*)(slot + wa[t]);
+    f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w[t]),
+                                                  __builtin_bit_cast(bf16x8, xr[t]), a, 0, 0, 0);
+    acc[j] = a;
+  }
+  // the quad sums (lane l's component l % 4: row l / 16 of the chunk, token (l % 16) / 4,
+  // quarter l % 4), one float a (row, token) at (l / 4) % 16 of the wave's slot
+  {
+    const int sel = lane & 3;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const f32x4 a = acc[j];
+      float x = sel == 0 ? a.x : sel == 1 ? a.y : sel == 2 ? a.z : a.w;
+      x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, false));
+      x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, false));
+      if (sel == 0) *(float*)(ring + RED + (wave * CPW + j) * 64 + (lane >> 2) * 4) = x;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  if (wave != 0 || fc >= CPW) return;
+  // lane l: chunk l / 16, row (l / 4) % 4, token l % 4
+  float v = 0.f;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) v += *(const float*)(ring + RED + (w2 * CPW + fc) * 64 + (lane & 15) * 4);
+  if (fused) v = act4(e.act, f32x4{v * sc + (ra_vec ? bf16_to_f32(bias_w) + e.cadd : add0), 0.f, 0.f, 0.f}).x;
+  if (f_ok && ftl < p.M) {
+    const int64_t idx = (int64_t)ftl * p.ldc + fn;
+    if (p.c_dt == HKX_BF16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+    else if (p.c_dt == HKX_FP16) ((uint16_t*)p.c)[idx] = (uint16_t)(pack_f16x2(v, 0.f) & 0xffffu);
+    else if (p.c_dt == HKX_FP32) ((float*)p.c)[idx] = v;
+    else if (p.c_dt == HKX_FP8E4M3) ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_e4m3(v);
+    else ((uint8_t*)p.c)[idx] = (uint8_t)f32_to_i8(v);
+  }
+}
+
 // The per-wave whole-row decode GEMM: K = 512 KS (KS = 2 or 4: K = 1024 or 2048), M <= 2
 // (M <= 3 at K = 1024), the fast epilogue form without a tile operand. The workgroups take chunks of 8
 // consecutive rows of W strided over the grid (workgroup g: chunks g, g + G, ...), and wave w
@@ -488,8 +619,21 @@ bool rows_takes(const DecodeArgs& a) {
   return a.g_total == 32 && a.M <= 4 && a.N <= 32768 && stream_fast(a) && !tile;
 }
 
+// The whole-row form a call runs: short workgroups of one chunk at M <= 2 and of two at
+// M = 3, and at M = 4 up to N = 8192; the persistent rows_kernel at M = 4 past that, where
+// each short workgroup's own copy of X (at M = 4 as many bytes as a chunk of W) costs more
+// than the dispatcher's balancing gains. Measured on one box, graph replays over four
+// rotated weights, K = 4096 (persistent -> short, us): N = 12288 M = 1 16.95 -> 16.18, M = 2
+// 17.01 -> 16.65, M = 4 17.15 -> 19.50 (one chunk) / 17.61 (two); N = 28672 M = 1 36.68 ->
+// 34.32; N = 6144 M = 4 10.63 -> 9.93 (two); N = 4096 M = 3 8.07 -> 7.21 (two).
 hipError_t launch_rows(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL(rows_kernel, grid, dim3(512), 0, s, a);
+  const int nck = (a.N + 3) / 4;
+  if (a.M <= 2)
+    hipLaunchKernelGGL(rowsq_kernel<1>, dim3(nck), dim3(512), 0, s, a);
+  else if (a.M == 3 || a.N <= 8192)
+    hipLaunchKernelGGL(rowsq_kernel<2>, dim3((nck + 1) / 2), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL(rows_kernel, grid, dim3(512), 0, s, a);
   return hipGetLastError();
 }
 

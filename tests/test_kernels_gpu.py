@@ -396,13 +396,16 @@ def test_decode_stream(m, nk):
     assert (c[:, n:].float() == 7.0).all()
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 5, 8, 9, 13, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 13, 16])
 @pytest.mark.parametrize("n", [12288, 1004, 4100, 8])
 def test_decode_rows(m, n):
-    """The whole-row decode kernel at M <= 4 (K = 4096: chunks of 4 rows strided over the
-    workgroups), the stream kernel above: bias, chunk counts a workgroup from 1 up (1025
-    chunks: one workgroup with a group of one), a W of row stride K + 64, an output of row
-    stride N + 8 with sentinels (columns past N never written)."""
+    """The whole-row decode kernels at M <= 4 (K = 4096, chunks of 4 rows: short workgroups
+    of one chunk at M <= 2, of two at M = 3 and at M = 4 up to N = 8192 -- 1004 and 4100
+    rows end on a workgroup whose second chunk is past N --, the persistent kernel with
+    chunks strided over the workgroups at M = 4 and N = 12288), the stream kernel above:
+    bias, chunk counts a workgroup from 1 up (1025 chunks: one workgroup with a group of
+    one), a W of row stride K + 64, an output of row stride N + 8 with sentinels (columns
+    past N never written)."""
     k = 4096
     a, b = _data(m, n, k, seed=31)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
@@ -417,7 +420,7 @@ def test_decode_rows(m, n):
     assert (c[:, n:].float() == 7.0).all()
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 3, 4])
 @pytest.mark.parametrize("n", [16384, 20004, 32768])
 def test_decode_rows_bias_many_groups(m, n):
     """The whole-row decode kernel with a bias where a workgroup walks 4 or more groups of
