@@ -196,10 +196,11 @@ typedef struct HkxEpilogue {
 #define HKX_DEC_STREAM 1  /* one workgroup a CU streaming W (M <= 16, or M <= 32 from K =
                              2048; K a multiple of 1024 up to 32768, no split, unpaired): in
                              blocks of 16 rows, or, with no residual and no vector scale, in
-                             chunks of whole rows strided over the workgroups -- 4 rows at
-                             K = 4096, M <= 4, N <= 32768; 8 rows, one a wave, at K = 1024
-                             (M <= 3) and K = 2048 (M <= 2); other calls take the blocked
-                             kernel */
+                             chunks of whole rows -- 4 rows at K = 4096, M <= 4, N <= 32768
+                             (one or two chunks a short workgroup at M <= 3, and at M = 4 up
+                             to N = 8192; else strided over one workgroup a CU); 8 rows, one
+                             a wave, at K = 1024 (M <= 3) and K = 2048 (M <= 2); other calls
+                             take the blocked kernel */
 
 typedef struct HkxGemmArgs {
   const void* a; /* (M, K), row stride lda elements */
