@@ -35,7 +35,7 @@
 //
 // The MX form (fp8 with E8M0 block scales, bf16 C): each K-tile's 4 scale bytes a row reach
 // LDS with the B0 fill of every 4th K-tile, 16 bytes a row, through three rotating buffers;
-// a lane passes its fragment row's byte for its 32-K block to the scaled MFMA.
+// lane group g of a 16 x 16 x 128 MFMA passes its fragment row's byte for 32-K block g.
 //
 // The paired form (C = silu(gate) * up, B's gate and up rows pair_off apart) reads 64 gate
 // and 64 up rows a B quarter, so a wave's two 16-row B fragments of a block are the gate
@@ -75,14 +75,12 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   static_assert(!PAIR || (!FP8 && EPF == kEpNone && ACT == HKX_ACT_NONE), "the paired form is silu * up");
   static_assert(SMEM <= 160 * 1024, "LDS");
 
-  // Fragment layout: W32, the MX form, 32 x 32 x 64 scaled MFMAs (its E8M0 block scales
-  // follow that instruction's K blocks); every other form 16 x 16 fragments -- bf16
-  // 16 x 16 x 32, plain fp8 16 x 16 x 128 (the K-tile's 128 bytes in one MFMA). The fp8
-  // 16 x 16 x 128 MFMA runs 9% more flops than 32 x 32 x 64 on random operands under the
-  // board's power limit (4.34 against 3.97 PFLOP/s, a register-only loop on one box), for
-  // the same operand registers, accumulators and LDS reads a K-tile.
-  constexpr bool W32 = MX;
-  constexpr int KH = FP8 && !MX ? 1 : 2;  // MFMA K-steps a fragment a K-tile
+  // Fragments are 16 x 16: bf16 on v_mfma_f32_16x16x32_bf16, fp8 (plain and MX) on
+  // v_mfma_scale_f32_16x16x128_f8f6f4, the K-tile's 128 bytes in one MFMA. The fp8 16 x 16 x 128
+  // MFMA runs 9% more flops than 32 x 32 x 64 on random operands under the board's power
+  // limit (4.34 against 3.97 PFLOP/s, a register-only loop on one box), for the same operand
+  // registers, accumulators and LDS reads a K-tile.
+  constexpr int KH = FP8 ? 1 : 2;  // MFMA K-steps a fragment a K-tile
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
@@ -215,36 +213,26 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
         (uint32_t)lane * 16u, __builtin_amdgcn_readfirstlane(so), 0, 0);
   };
 
-  // ---- fragment reads. bf16 (16 x 16 x 32): lane l reads row l % 16 of a 16-row
-  // fragment, 16-byte chunk l / 16 of the K-half; a fragment of quarter rows r0..
-  // (r0 % 16 == 0) at K-half s sits at r0 * 128 + s * 512 + rdo[(r0 >> 4) & 1]. fp8
-  // (32 x 32 x 64): lane l reads row l % 32 of a 32-row fragment, chunks h and 2 + h of the
-  // K-half (h = l / 32): the scaled MFMA takes a lane's bytes 0-15 as K block 0 of its 64
-  // and 16-31 as block 1, so lane half h holds K [16 h, +16) of each 32-K block; at
-  // r0 * 128 + s * 512 + rdo[0 or 1].
+  // ---- fragment reads. Lane l reads row l % 16 of a 16-row fragment, 16-byte chunk l / 16
+  // of a K-half; a fragment of quarter rows r0.. (r0 % 16 == 0) at K-half s sits at
+  // r0 * 128 + s * 512 + rdo[(r0 >> 4) & 1]. bf16 (16 x 16 x 32) takes one K-half an MFMA;
+  // fp8 (16 x 16 x 128) the chunk of both, the MFMA taking a lane's bytes 0-15 as K
+  // 16 (l / 16) + [0, 16) and bytes 16-31 as K 64 + 16 (l / 16) + [0, 16) -- so lane group
+  // l / 16 holds half of each of the K-tile's 32-K blocks l / 16 / 2 and 2 + l / 16 / 2, and
+  // the MX form's scale of 32-K block b comes from lane group b.
   uint32_t rdo[2];
-  if constexpr (W32) {
-    const int rf = lane & 31, h = lane >> 5;
-    const int sw = ((rf >> 4) & 1) | (((rf >> 3) & 1) << 1);
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      rdo[q] = (uint32_t)((rf >> 3) * 1024 + (rf & 7) * 64 + (((2 * q + h) ^ sw) << 4));
-  } else {
+  {
     const int rr = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int par = 0; par < 2; ++par)
       rdo[par] = (uint32_t)((rr >> 3) * 1024 + (rr & 7) * 64 + ((q ^ (par | ((rr >> 3) << 1))) << 4));
   }
-  constexpr int NA = W32 ? 2 : 4, NB = W32 ? 1 : 2;  // fragments of a block's A and B rows
+  constexpr int NA = 4, NB = 2;  // 16-row fragments of a block's 64 A rows and 32 B rows
   using Frag = typename std::conditional<FP8, i32x8, bf16x8>::type;
   // [fragment][K-half]; bfn: B1 of the next K-tile (see the K loop)
   Frag af[NA][2], bf0[NB][2], bf1[NB][2], bfn[NB][2];
   auto frag_at = [&](const uint8_t* s, int r0, int h, int par) -> Frag {
-    if constexpr (W32) {
-      const i32x4 lo = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[0]);
-      const i32x4 hi = *(const i32x4*)(s + r0 * 128 + h * 512 + rdo[1]);
-      return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    } else if constexpr (FP8) {
+    if constexpr (FP8) {
       // 16 x 16 x 128: the bf16 fragment's 16-byte chunk of both K-halves, so lane l holds
       // K 16 (l / 16) + [0, 16) and 64 + 16 (l / 16) + [0, 16) of row l % 16 -- in A and B
       // alike, which is all a dot product needs of the K order
@@ -271,25 +259,26 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
   };
 
   // MX: the E8M0 dword of each of this lane's fragment rows for the K-tile (its 4 blocks,
-  // byte 2 s + h for K-half s and lane half h), read at the K-tile's first phase and shifted
-  // down a byte in lane half 1, so K-half s's scale is byte 2 s in every lane: the MFMA
-  // takes it by its byte select (op_sel), with no shift per MFMA
-  [[maybe_unused]] uint32_t sca[2][2], scb[2];  // [A half][fragment], [B half]
-  const int sc_sh = 8 * (lane >> 5);
+  // byte b for 32-K block b), read at the K-tile's first phase and shifted down by lane group
+  // (l / 16) bytes, so every lane's byte 0 is the scale of the block its group supplies
+  [[maybe_unused]] uint32_t sca[2][4], scb[2][2];  // [A half][fragment], [B half][fragment]
+  const int sc_sh = 8 * (lane >> 4);
   auto read_scales = [&](int lt, int t) {
     if constexpr (MX) {
       const uint32_t* sc = (const uint32_t*)(smem + SCO + ((lt * cpt + (t >> 2)) % 3) * 8192) + (t & 3);
-      const int rf = lane & 31;
+      const int rf = lane & 15;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int f = 0; f < 2; ++f) sca[i][f] = sc[4 * (128 * i + 64 * grp + 32 * f + rf)] >> sc_sh;
+        for (int f = 0; f < 4; ++f) sca[i][f] = sc[4 * (128 * i + 64 * grp + 16 * f + rf)] >> sc_sh;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) scb[j] = sc[4 * (256 + 128 * j + 32 * wc + rf)] >> sc_sh;
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) scb[j][g] = sc[4 * (256 + 128 * j + 32 * wc + 16 * g + rf)] >> sc_sh;
     }
   };
 
-  using Acc = typename std::conditional<W32, f32x16, f32x4>::type;
+  using Acc = f32x4;
   Acc acc[NI][2][NA][NB];  // [A half][B half][row fragment][column fragment]
   auto math = [&](int i, int j, const Frag (&bf)[NB][2], bool zero) {
     __builtin_amdgcn_s_setprio(1);
@@ -300,14 +289,9 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
 #pragma unroll
         for (int g = 0; g < NB; ++g) {
           const Acc c = (zero && h == 0) ? Acc{} : acc[i][j][f][g];
-          if constexpr (MX) {
-            if (h == 0)
-              acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                  bf[g][h], af[f][h], c, 0, 0, 0, (int)scb[j], 0, (int)sca[i][f]);
-            else
-              acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                  bf[g][h], af[f][h], c, 0, 0, 2, (int)scb[j], 2, (int)sca[i][f]);
-          }
+          if constexpr (MX)
+            acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                bf[g][h], af[f][h], c, 0, 0, 0, (int)scb[j][g], 0, (int)sca[i][f]);
           else if constexpr (FP8)
             acc[i][j][f][g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[g][h], af[f][h], c, 0, 0, 0,
                                                                                0, 0, 0);
@@ -351,56 +335,6 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
             }
       return;
     }
-    if constexpr (W32) {
-      // MX, 32 x 32 (no epilogue operands): lane l (row l % 32, half h = l / 32) holds
-      // columns 8 g + 4 h + [0, 4) in run g of a fragment's 16 values; runs 2 t and 2 t + 1
-      // trade halves (v_permlane32_swap), so lane l stores columns 16 t + 8 h + [0, 8)
-      const int h = lane >> 5;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        __builtin_amdgcn_sched_barrier(0);
-        const int cb = 128 * j + 32 * wc;  // the block's first column
-        // after the 16-lane trade below, lane l stores row 16 s + l % 16 of the fragment
-        // (s: which of the two registers), columns 16 ((l >> 4) & 1) + 8 (l >> 5) + [0, 8)
-        // of the block: each store covers 16 rows x 64 contiguous bytes (four lanes a row),
-        // not 32 rows x 32 bytes (a 33 MB burst of C measured 2.9 TB/s in 32-byte pieces,
-        // 3.3 in 64-byte ones)
-        const int n = cb + 16 * ((lane >> 4) & 1) + 8 * (lane >> 5);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int f = 0; f < 2; ++f) {
-            uint32_t T[2][4];  // [run t]: lane (rf, h)'s columns 16 t + 8 h + [0, 8) of row rf
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              f32x4 v[2];
-#pragma unroll
-              for (int u = 0; u < 2; ++u) {
-                const Acc& a = acc[i][j][f][0];
-                const int r = 8 * t + 4 * u;
-                v[u] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
-              }
-              const u32x2 w0 = pack4<2>(HKX_BF16, v[0]), w1 = pack4<2>(HKX_BF16, v[1]);
-              uint32_t x0 = w0.x, x1 = w1.x, y0 = w0.y, y1 = w1.y;
-              swap32(x0, x1);
-              swap32(y0, y1);
-              T[t][0] = x0;
-              T[t][1] = y0;
-              T[t][2] = x1;
-              T[t][3] = y1;
-            }
-            // rows 0-15 of both runs into T[0], rows 16-31 into T[1]
-#pragma unroll
-            for (int d = 0; d < 4; ++d) swap16(T[0][d], T[1][d]);
-#pragma unroll
-            for (int sr = 0; sr < 2; ++sr) {
-              const int ml = 128 * i + 64 * grp + 32 * f + 16 * sr + (lane & 15);
-              store_c(i32x4{(int)T[sr][0], (int)T[sr][1], (int)T[sr][2], (int)T[sr][3]}, n0 + n < p.N,
-                      (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u);
-            }
-          }
-      }
-    } else {
     const int rf = lane & 15, q = lane >> 4;
     // fp8 dequant: this lane's row scales [i][f] (row 128 i + 64 grp + 16 f + rf) and the
     // column scales of its columns [j][g] (as the bias), read once a tile
@@ -512,7 +446,6 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
                   (uint32_t)(m0 + ml) * row_b + (uint32_t)(n0 + n) * 2u);
         }
       }
-    }
   };
 
   // ---- the K loop. Before the first phase: K-tile 0 whole and K-tile 1 but A1, in the
@@ -614,7 +547,8 @@ __global__ void __launch_bounds__(512, 1) quad_kernel(const TileArgs p) {
     // other's stores), where group 0's epilogue used to hold group 1 at that barrier for the
     // epilogue's whole length (config 5 1.2%, config 2 0.6% faster, same box). Nothing in
     // between reads LDS but the epilogue's own vector slot, which no fill of that interval
-    // touches. (The MX form keeps the plain order.)
+    // touches. (The MX form keeps the plain order: the early epilogue made it 9-14% slower,
+    // same box, 2048-8192 rows.)
     constexpr bool EARLY = !MX;
     auto ktile = [&](int lt, int t, int g, Frag (&b1)[NB][2], Frag (&nb1)[NB][2]) {
       const int slot = g & 1;
