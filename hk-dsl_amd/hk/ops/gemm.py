@@ -4,9 +4,10 @@
 (A @ B^T) * scale_a * scale_b (+ bias), A (M, K) and B (N, K) float8_e4m3fn, fp32
 accumulate; scale_a one value or one a row of A ((M,) or (M, 1)), scale_b one value or
 one a row of B ((N,) or (1, N)); bias (N,). The reference runs it on gfx1201 only (its
-gfx950 fp8 GEMMs are MX block-scaled); here it is the tile kernel's fp8 form,
-v_mfma_f32_32x32x64_f8f6f4 with the scales and the bias applied to the accumulators in
-registers before the one bf16 store.
+gfx950 fp8 GEMMs are MX block-scaled); here it is the tile kernels' fp8 forms (at 256 x 256
+the quadrant kernel on v_mfma_f32_16x16x128_f8f6f4, smaller tiles on the 4-wave and 8-wave
+kernels) with the scales and the bias applied to the accumulators in registers before the
+one bf16 store.
 """
 
 from __future__ import annotations
