@@ -610,13 +610,18 @@ hipError_t launch_roww(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Whether the whole-row kernel takes a call the stream kernel takes: K = 4096, M <= 4, N up
-// to 32768, the fast epilogue form without a tile operand (every chunk's byte offset then
-// fits 32 bits). At the LM head's N (151936) it measured 1% faster at M = 1 and 3% slower at
-// M = 4 than the stream kernel, whose long runs of blocks reach the same rate there.
+// Whether the whole-row kernels take a call the stream kernel takes: K = 4096, M <= 4, the
+// fast epilogue form without a tile operand; N up to 32768, and at M <= 2 (the short
+// workgroups of one chunk) any N whose W spans less than 2 GiB (chunk offsets and the
+// out-of-range fill offset within 31 bits). At the LM heads' N the short workgroups beat the
+// stream kernel at M = 1 (151936 x 4096: 177.7 against 189.2 us, 7.0 TB/s; 128256: 150.3
+// against 156.4; 65536: 75.3 against 82.3, one box) and tie or win at M = 2; from M = 3
+// (two chunks a workgroup, or the persistent kernel) they lose there (151936 at M = 4:
+// 194.2 against 189.5), so those stay at N <= 32768.
 bool rows_takes(const DecodeArgs& a) {
   const bool tile = a.ep.form == HKX_EP_FUSED && a.ep.ta.p;
-  return a.g_total == 32 && a.M <= 4 && a.N <= 32768 && stream_fast(a) && !tile;
+  const bool n_ok = a.M <= 2 ? (int64_t)a.N * a.ldb_b < (1LL << 31) : a.N <= 32768;
+  return a.g_total == 32 && a.M <= 4 && n_ok && stream_fast(a) && !tile;
 }
 
 // The whole-row form a call runs: short workgroups of one chunk at M <= 2 and of two at

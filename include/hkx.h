@@ -197,8 +197,9 @@ typedef struct HkxEpilogue {
                              2048; K a multiple of 1024 up to 32768, no split, unpaired): in
                              blocks of 16 rows, or, with no residual and no vector scale, in
                              chunks of whole rows -- 4 rows at K = 4096, M <= 4, N <= 32768
-                             (one or two chunks a short workgroup at M <= 3, and at M = 4 up
-                             to N = 8192; else strided over one workgroup a CU); 8 rows, one
+                             or at M <= 2 any N with W under 2 GiB (one or two chunks a short
+                             workgroup at M <= 3, and at M = 4 up to N = 8192; else strided
+                             over one workgroup a CU); 8 rows, one
                              a wave, at K = 1024 (M <= 3) and K = 2048 (M <= 2); other calls
                              take the blocked kernel */
 

@@ -420,13 +420,14 @@ def test_decode_rows(m, n):
     assert (c[:, n:].float() == 7.0).all()
 
 
-@pytest.mark.parametrize("m", [1, 3, 4])
-@pytest.mark.parametrize("n", [16384, 20004, 32768])
+@pytest.mark.parametrize("m,n", [(m, n) for m in (1, 3, 4) for n in (16384, 20004, 32768)]
+                         + [(1, 40004), (2, 40004), (1, 65540)])
 def test_decode_rows_bias_many_groups(m, n):
     """The whole-row decode kernel with a bias where a workgroup walks 4 or more groups of
     chunks (N > 12288 on 256 CUs), so the three bias slots of its LDS are each reused: a
     DMA of one group's bias words must leave the other slots' words alone (N = 20004 also
-    ends on a ragged chunk)."""
+    ends on a ragged chunk); past N = 32768 at M <= 2, the short-workgroup form that the LM
+    heads' N takes (N = 40004 and 65540 here)."""
     k = 4096
     a, b = _data(m, n, k, seed=36)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(37)).to(torch.bfloat16)
