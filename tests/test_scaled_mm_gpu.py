@@ -77,10 +77,12 @@ def test_e5m2_needs_the_ring_kernels_n():
         hk.ops.scaled_mm(a8.to(DEV), b8.to(DEV), sa.to(DEV), sb.to(DEV))
 
 
-@pytest.mark.parametrize("m,n,k,route", [(128, 4096, 4096, "t64x128k2"), (64, 1024, 8192, "t64x128k4")])
+@pytest.mark.parametrize("m,n,k,route", [(128, 4096, 4096, "t64x128k2"), (64, 1024, 8192, "t64x128k4"),
+                                         (256, 4096, 4096, "t64x128"), (384, 2048, 8192, "t64x128k2")])
 def test_mid_m_splits_over_k(m, n, k, route):
-    # fp8 takes the route rule; at these shapes it splits 64 x 128 tiles over K (fp32
-    # shares summed in split order, then the dequant and the bias)
+    # fp8 takes the route rule; at these shapes it runs 64 x 128 tiles, split over K where
+    # each split keeps enough K (fp32 shares summed in split order, then the dequant and the
+    # bias)
     from hk.ops import gemm_cdna
 
     assert gemm_cdna.route(m, n, k, fp8=True) == route
