@@ -655,7 +655,10 @@ def other_configs(steps, warmup, peaks):
                 calls = [lambda w=ws[i % 4]: T(x, w, epilogue=T.bias, bias=bias, out=y) for i in range(32)]
             else:
                 calls = [lambda w=ws[i % 4]: T(x, w, out=y) for i in range(32)]
-            # ~20 us launches: timed as a graph of 32 calls, the host's call overhead out
+            # ~20 us launches: timed as a graph of 32 calls, the host's call overhead out,
+            # after the same untimed ramp as the other arms
+            if RAMP_S > 0:
+                _ramp(calls[0], RAMP_S)
             t = _graph_time(calls)
             byts = 12288 * 4096 * 2 + m * 4096 * 2 + m * 12288 * 2 + (12288 * 2 if epi == "bias" else 0)
             out[f"cfg4_decode_M{m}_{epi}"] = {"GB/s": round(byts / t / 1e9, 1),
